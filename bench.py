@@ -1,0 +1,361 @@
+#!/usr/bin/env python3
+"""Benchmark of the depthwise causal conv1d hot path on one MI355X.
+
+Workload (the config the metric is quoted on):
+  C2: x (4, 5120, 2048) bf16 channel-first, weight (5120, 4), bias (5120),
+      SiLU, dout N(0,1); one step = forward + backward through the public API
+      (causal_conv1d_fn + torch.autograd.grad), captured as one HIP graph per
+      rotating buffer set so that the step time is GPU time.
+
+Reported (one JSON line):
+  value        step throughput in GB/s = algorithmic bytes of the forward and
+               backward kernels (167,823,360 + 251,811,840 B) / step time
+  roofline     for the dominant kernel (the fused backward): algorithmic bytes
+               per launch / average launch duration, measured here with HIP
+               events around a graph of back-to-back launches, vs 8 TB/s.
+               `traffic` (HBM bytes per launch) is read from the rocprofv3
+               --pmc summary committed in profiles/ when present.
+  kernels      the same measurement for the forward kernel and for the decode
+               update (C4a: 256 x 5120 bf16, pool 512 x 5120 x 3, random rows),
+               in GB/s and microseconds per call.
+  cpu_baseline the CPU oracle (C restatement of the reference's CPU kernels,
+               OpenMP) on a bounded sample of C2, on this host.
+
+Input sets are rotated so that the data touched between two reuses of a
+buffer exceeds the 256 MB Infinity Cache: every launch streams from HBM.
+
+Modes: --mode bench (default), --mode kernels (eager launch loop for
+rocprofv3 --kernel-trace / --pmc), --mode copy (a plain 1 GiB device copy,
+the calibration kernel for FETCH_SIZE / WRITE_SIZE).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "causal-conv1d-mojo_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "fwd/bwd achieved HBM GB/s (% peak) at B4×D5120×L2048 bf16; update µs/call"
+HBM_PEAK_GBPS = 8000.0
+B, D, L, W = 4, 5120, 2048, 4
+# algorithmic bytes: every input read once, every output written once
+FWD_BYTES = 2 * B * D * L * 2 + D * W * 2 + D * 2                      # 167,823,360
+BWD_BYTES = 3 * B * D * L * 2 + D * W * 2 + D * 2 + D * W * 4 + D * 4  # 251,811,840
+UPD_B, UPD_POOL = 256, 512
+UPD_BYTES = UPD_B * D * (2 + 6 + 6 + 2) + D * W * 2 + D * 2 + UPD_B * 4  # 21,023,744
+MALL_BYTES = 256 * 2 ** 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--mode", choices=["bench", "kernels", "copy"], default="bench")
+    ap.add_argument("--launches", type=int, default=40, help="launches per kernel timing graph")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
+    return ap.parse_args()
+
+
+def _c2_sets(torch, n):
+    sets = []
+    for i in range(n):
+        g = torch.Generator(device="cuda").manual_seed(100 + i)
+        x = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
+        dout = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
+        sets.append((x, dout))
+    g = torch.Generator(device="cuda").manual_seed(0)
+    w = torch.randn(D, W, generator=g, device="cuda").bfloat16()
+    b = torch.randn(D, generator=g, device="cuda").bfloat16()
+    return sets, w, b
+
+
+def _graph(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def _time_graph(torch, g, reps):
+    """Average ms per replay over `reps` replays, HIP events on torch's current stream."""
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
+
+
+def _pmc_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+    p = ROOT / "profiles" / "pmc_summary.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def bench_step(torch, cc, args):
+    nsets = max(2, -(-MALL_BYTES // (4 * B * D * L * 2)) + 1)
+    sets, w, b = _c2_sets(torch, nsets)
+    params = [w.requires_grad_(), b.requires_grad_()]
+
+    def make_step(x, dout):
+        xl = x.requires_grad_()
+
+        def step():
+            out = cc.causal_conv1d_fn(xl, params[0], params[1], activation="silu")
+            torch.autograd.grad(out, (xl, params[0], params[1]), dout)
+
+        return step
+
+    graphs = [_graph(torch, make_step(x, dout)) for x, dout in sets]
+    for i in range(args.warmup):
+        graphs[i % nsets].replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record()
+    for i in range(args.steps):
+        graphs[i % nsets].replay()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / args.steps
+    log(f"step: {ms * 1e3:.1f} us/step over {args.steps} steps ({nsets} buffer sets, wall {wall:.3f} s)")
+    del graphs
+    return ms, sets, w.detach(), b.detach()
+
+
+def bench_kernels(torch, sets, w, b, launches):
+    """Per-launch duration of the forward and backward kernels (custom ops, no autograd)."""
+    nsets = len(sets)
+    outs = [torch.empty_like(x) for x, _ in sets]
+    dxs = [torch.empty_like(x) for x, _ in sets]
+    dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
+    db = torch.zeros(D, dtype=torch.float32, device="cuda")
+    xs = [x.detach() for x, _ in sets]
+
+    def fwd_loop():
+        for i in range(launches):
+            torch.ops.causal_conv1d_amd._fwd_inplace(xs[i % nsets], w, b, None, None, outs[i % nsets], True, None)
+
+    def bwd_loop():
+        for i in range(launches):
+            x, dout = xs[i % nsets], sets[i % nsets][1]
+            torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dxs[i % nsets], dw, db, None,
+                                                          True)
+
+    res = {}
+    for name, loop, nbytes in (("fwd", fwd_loop, FWD_BYTES), ("bwd", bwd_loop, BWD_BYTES)):
+        g = _graph(torch, loop)
+        ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
+        res[name] = {"us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                     "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"{name}: {res[name]}")
+        del g
+    return res
+
+
+def _update_sets(torch, n):
+    sets = []
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w = torch.randn(D, W, generator=g, device="cuda").bfloat16()
+    b = torch.randn(D, generator=g, device="cuda").bfloat16()
+    for _ in range(n):
+        x = torch.randn(UPD_B, D, generator=g, device="cuda").bfloat16()
+        pool = torch.randn(UPD_POOL, D, W - 1, generator=g, device="cuda").bfloat16()
+        idx = torch.randperm(UPD_POOL, generator=g, device="cuda")[:UPD_B].to(torch.int32)
+        sets.append((x, pool, idx, torch.empty_like(x)))
+    return sets, w, b
+
+
+def bench_update(torch, cc, launches):
+    nsets = -(-MALL_BYTES // (UPD_POOL * D * (W - 1) * 2 + 2 * UPD_B * D * 2)) + 1
+    sets, w, b = _update_sets(torch, nsets)
+    lib_update = cc._native.native_update
+
+    def loop():
+        for i in range(launches):
+            x, pool, idx, out = sets[i % nsets]
+            lib_update(x.unsqueeze(-1), w, b, pool, idx, None, out.unsqueeze(-1), True)
+
+    g = _graph(torch, loop)
+    ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
+    us = ms * 1e3
+    res = {"workload": "C4a: x (256,5120,1) bf16, pool (512,5120,3), 256 random rows, W4, bias, SiLU",
+           "us_per_call": round(us, 2), "algorithmic_bytes": UPD_BYTES,
+           "gbps": round(UPD_BYTES / (us * 1e-6) / 1e9, 1),
+           "frac_of_peak": round(UPD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "buffer_sets": nsets}
+    log(f"update: {res}")
+    return res
+
+
+def cpu_baseline(torch, seconds):
+    """The CPU oracle on a bounded sample of C2 (512 of the 5120 channels, all 4
+    batches, full length), fwd + bwd repeated for about `seconds`."""
+    from oracle import oracle as O
+
+    d = 512
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, d, L, generator=g).bfloat16()
+    w = torch.randn(d, W, generator=g).bfloat16()
+    b = torch.randn(d, generator=g).bfloat16()
+    dout = torch.randn(B, d, L, generator=g).bfloat16()
+    out = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    nbytes = (FWD_BYTES + BWD_BYTES) * d / D
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.fwd(x, w, b, None, None, out, True)
+        dw = torch.zeros(d, W)
+        db = torch.zeros(d)
+        O.bwd(x, w, b, dout, None, None, dx, dw, db, None, True)
+        reps += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and reps >= 3) or reps >= 10000:
+            break
+    per = el / reps
+    res = {"value": round(nbytes / per / 1e9, 2), "unit": "GB/s", "cores": O.num_threads(), "kind": "port",
+           "sample": f"C2 fwd+bwd restricted to 512 of 5120 channels (x (4,512,2048) bf16), {reps} reps "
+                     f"in {el:.1f} s, {per * 1e3:.1f} ms per fwd+bwd; C oracle restating the reference's "
+                     f"Mojo CPU kernels (the Mojo path itself cannot be built here)",
+           "cpu_model": _cpu_model()}
+    log(f"cpu baseline: {res}")
+    return res
+
+
+def _cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def mode_kernels(torch, cc, args):
+    """Eager launch loop (for rocprofv3 kernel traces / counters)."""
+    sets, w, b = _c2_sets(torch, 3)
+    outs = [torch.empty_like(x) for x, _ in sets]
+    dxs = [torch.empty_like(x) for x, _ in sets]
+    dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
+    db = torch.zeros(D, dtype=torch.float32, device="cuda")
+    usets, uw, ub = _update_sets(torch, 13)
+    for i in range(args.steps):
+        x, dout = sets[i % 3]
+        torch.ops.causal_conv1d_amd._fwd_inplace(x, w, b, None, None, outs[i % 3], True, None)
+        torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dxs[i % 3], dw, db, None, True)
+        ux, pool, idx, uo = usets[i % 13]
+        cc._native.native_update(ux.unsqueeze(-1), uw, ub, pool, idx, None, uo.unsqueeze(-1), True)
+    torch.cuda.synchronize()
+    log(f"kernels mode: {args.steps} iterations of fwd + bwd + update done")
+
+
+def mode_copy(torch, args):
+    n = 2 ** 30 // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    c = torch.empty_like(a)
+    for _ in range(args.steps):
+        c.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy mode: {args.steps} copies of 1 GiB done")
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the op needs no "
+              f"collectives and every GPU box here has a single MI355X.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    import causal_conv1d_amd as cc
+    from causal_conv1d_amd import _lib
+
+    _lib.load()  # fail loudly if the HIP library is missing
+    if args.mode == "kernels":
+        return mode_kernels(torch, cc, args)
+    if args.mode == "copy":
+        return mode_copy(torch, args)
+
+    ms, sets, w, b = bench_step(torch, cc, args)
+    kern = bench_kernels(torch, sets, w, b, args.launches)
+    del sets
+    torch.cuda.empty_cache()
+    upd = bench_update(torch, cc, args.launches)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch, args.cpu_seconds)
+
+    step_bytes = FWD_BYTES + BWD_BYTES
+    value = step_bytes / (ms * 1e-3) / 1e9
+    bwd = kern["bwd"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: causal_conv1d_fn fwd + autograd bwd, x (4,5120,2048) bf16 channel-first, "
+                        "weight (5120,4), bias, SiLU; one HIP graph per rotating buffer set",
+            "batch": B, "dim": D, "seqlen": L, "width": W, "accumulate": "fp32",
+            "step_algorithmic_bytes": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "bwd_rows_vec (fused backward)",
+            "achieved": bwd["gbps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(bwd["gbps"] / HBM_PEAK_GBPS, 4),
+            "traffic": _pmc_traffic("bwd"),
+            "algorithmic_bytes_per_launch": BWD_BYTES,
+            "us_per_launch": bwd["us_per_launch"],
+        },
+        "kernels": {"fwd": kern["fwd"], "bwd": kern["bwd"], "update_c4a": upd},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,119 @@
+"""ctypes binding of ``libcc1d_amd.so`` (the C ABI in ``include/cc1d.h``).
+
+The structures below mirror ``cc1d_fwd_params`` / ``cc1d_bwd_params`` /
+``cc1d_update_params`` / ``cc1d_varlen_params`` field for field. The library
+is loaded on first use; a missing or stale build raises instead of falling
+back to anything else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
+ABI_VERSION = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_vp = ctypes.c_void_p
+_i64x2 = _i64 * 2
+_i64x3 = _i64 * 3
+
+
+class FwdParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("weight", _vp), ("bias", _vp), ("seq_idx", _vp), ("initial_states", _vp),
+        ("out", _vp), ("final_states_out", _vp),
+        ("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("width", _i64),
+        ("x_stride", _i64x3), ("weight_stride", _i64x2), ("bias_stride", _i64),
+        ("seq_idx_stride", _i64x2), ("initial_states_stride", _i64x3), ("out_stride", _i64x3),
+        ("final_states_stride", _i64x3),
+        ("dtype", _i32), ("apply_silu", _i32),
+    ]
+
+
+class BwdParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("weight", _vp), ("bias", _vp), ("dout", _vp), ("seq_idx", _vp),
+        ("initial_states", _vp), ("dfinal_states", _vp),
+        ("dx", _vp), ("dweight_acc", _vp), ("dbias_acc", _vp), ("dinitial_states", _vp),
+        ("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("width", _i64),
+        ("x_stride", _i64x3), ("weight_stride", _i64x2), ("bias_stride", _i64), ("dout_stride", _i64x3),
+        ("seq_idx_stride", _i64x2), ("initial_states_stride", _i64x3), ("dfinal_states_stride", _i64x3),
+        ("dx_stride", _i64x3), ("dweight_acc_stride", _i64x2), ("dbias_acc_stride", _i64),
+        ("dinitial_states_stride", _i64x3),
+        ("dtype", _i32), ("apply_silu", _i32),
+    ]
+
+
+class UpdateParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("weight", _vp), ("bias", _vp), ("conv_state", _vp), ("conv_state_indices", _vp),
+        ("cache_seqlens", _vp), ("out", _vp),
+        ("batch", _i64), ("dim", _i64), ("seqlen", _i64), ("width", _i64), ("state_len", _i64),
+        ("state_rows", _i64),
+        ("x_stride", _i64x3), ("weight_stride", _i64x2), ("bias_stride", _i64),
+        ("conv_state_stride", _i64x3), ("out_stride", _i64x3),
+        ("dtype", _i32), ("apply_silu", _i32),
+    ]
+
+
+class VarlenParams(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp), ("cu_seqlens", _vp), ("states", _vp),
+        ("total_tokens", _i64), ("dim", _i64), ("batch", _i64), ("state_len", _i64),
+        ("x_stride", _i64x2), ("states_stride", _i64x3),
+        ("dtype", _i32), ("reserved", _i32),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "cc1d_abi_version",
+    "cc1d_strerror",
+    "cc1d_fwd",
+    "cc1d_bwd",
+    "cc1d_update",
+    "cc1d_varlen_states",
+)
+
+_lib = None
+
+
+def library_path() -> Path:
+    return Path(os.environ.get("CC1D_AMD_LIB", _LIB_PATH))
+
+
+def load():
+    """Load and type the shared library (cached). Raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"causal_conv1d_amd: native library {path} is not built; "
+            "run `python causal-conv1d-mojo_amd/csrc/build.py`"
+        )
+    lib = ctypes.CDLL(str(path))
+    lib.cc1d_abi_version.restype = ctypes.c_int
+    lib.cc1d_abi_version.argtypes = []
+    lib.cc1d_strerror.restype = ctypes.c_char_p
+    lib.cc1d_strerror.argtypes = [ctypes.c_int]
+    for name, st in (("cc1d_fwd", FwdParams), ("cc1d_bwd", BwdParams), ("cc1d_update", UpdateParams),
+                     ("cc1d_varlen_states", VarlenParams)):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(st), _vp]
+    got = lib.cc1d_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"causal_conv1d_amd: ABI version mismatch (library {got}, bindings {ABI_VERSION})")
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = load().cc1d_strerror(status).decode()
+        raise RuntimeError(f"causal_conv1d_amd native call failed: {msg} (status {status})")

@@ -1,0 +1,111 @@
+// cc1d_abi.hip -- extern "C" entry points declared in include/cc1d.h.
+//
+// Validates the plain-pointer arguments, handles zero-size problems, and
+// forwards to the kernel launchers on the caller's stream. No allocation, no
+// synchronisation, no exceptions across the boundary.
+#include "cc1d_internal.hpp"
+
+using namespace cc1d;
+
+namespace {
+
+constexpr int64_t kMaxBlocks = (int64_t)1 << 31;
+
+bool valid_dtype(int32_t d) { return d == CC1D_DTYPE_FP16 || d == CC1D_DTYPE_BF16 || d == CC1D_DTYPE_FP32; }
+bool valid_width(int64_t w) { return w >= 2 && w <= 9; }
+int esize(int32_t d) { return d == CC1D_DTYPE_FP32 ? 4 : 2; }
+
+// Every launcher uses at most one thread per element of the largest tensor
+// it touches; refuse problems whose grids would not fit.
+bool grid_fits(int64_t threads) { return threads / 256 + 1 < kMaxBlocks; }
+
+}  // namespace
+
+extern "C" {
+
+int cc1d_abi_version(void) { return CC1D_ABI_VERSION; }
+
+const char* cc1d_strerror(int status) {
+    switch (status) {
+    case CC1D_OK: return "ok";
+    case CC1D_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case CC1D_ERR_DTYPE: return "unsupported dtype code (expected 0=fp16, 1=bf16, 2=fp32)";
+    case CC1D_ERR_WIDTH: return "width must be in 2..9";
+    case CC1D_ERR_SHAPE: return "invalid or too large shape";
+    case CC1D_ERR_EXCLUSIVE: return "seq_idx is mutually exclusive with initial_states and final_states";
+    case CC1D_ERR_STATE_LEN: return "conv_state length must be >= width - 1";
+    case CC1D_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+    }
+}
+
+int cc1d_fwd(const cc1d_fwd_params* p, void* stream) {
+    if (p == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
+    if (p->seq_idx != nullptr && (p->initial_states != nullptr || p->final_states_out != nullptr))
+        return CC1D_ERR_EXCLUSIVE;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p->batch == 0 || p->dim == 0) return CC1D_OK;
+    if (!grid_fits(p->batch * p->dim * (p->seqlen > 0 ? p->seqlen : 1))) return CC1D_ERR_SHAPE;
+    if (p->seqlen == 0) {
+        if (p->final_states_out == nullptr) return CC1D_OK;
+        return launch_zero3(p->final_states_out, esize(p->dtype), p->batch, p->dim, p->width - 1,
+                            p->final_states_stride, s);
+    }
+    if (p->x == nullptr || p->weight == nullptr || p->out == nullptr) return CC1D_ERR_NULL_POINTER;
+    return launch_fwd(*p, s);
+}
+
+int cc1d_bwd(const cc1d_bwd_params* p, void* stream) {
+    if (p == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
+    if (p->seq_idx != nullptr && (p->initial_states != nullptr || p->dfinal_states != nullptr))
+        return CC1D_ERR_EXCLUSIVE;
+    if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p->batch == 0 || p->dim == 0) return CC1D_OK;
+    if (!grid_fits(p->batch * p->dim * (p->seqlen > 0 ? p->seqlen : 1))) return CC1D_ERR_SHAPE;
+    if (p->seqlen == 0) {
+        // no positions: dx is empty, the accumulators receive nothing and
+        // dinitial_states (a sum over no terms) is zero
+        if (p->dinitial_states == nullptr) return CC1D_OK;
+        return launch_zero3(p->dinitial_states, esize(p->dtype), p->batch, p->dim, p->width - 1,
+                            p->dinitial_states_stride, s);
+    }
+    if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr ||
+        p->dweight_acc == nullptr)
+        return CC1D_ERR_NULL_POINTER;
+    return launch_bwd(*p, s);
+}
+
+int cc1d_update(const cc1d_update_params* p, void* stream) {
+    if (p == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0 || p->state_len < 0 || p->state_rows < 0)
+        return CC1D_ERR_SHAPE;
+    if (p->state_len < p->width - 1) return CC1D_ERR_STATE_LEN;
+    if (p->conv_state_indices == nullptr && p->state_rows < p->batch) return CC1D_ERR_SHAPE;
+    if (p->batch == 0 || p->dim == 0 || p->seqlen == 0) return CC1D_OK;
+    if (!grid_fits(p->batch * p->dim)) return CC1D_ERR_SHAPE;
+    if (p->x == nullptr || p->weight == nullptr || p->conv_state == nullptr || p->out == nullptr)
+        return CC1D_ERR_NULL_POINTER;
+    return launch_update(*p, static_cast<hipStream_t>(stream));
+}
+
+int cc1d_varlen_states(const cc1d_varlen_params* p, void* stream) {
+    if (p == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (p->total_tokens < 0 || p->dim < 0 || p->batch < 0 || p->state_len < 0) return CC1D_ERR_SHAPE;
+    if (p->batch == 0 || p->dim == 0 || p->state_len == 0) return CC1D_OK;
+    if (!grid_fits(p->batch * p->dim * p->state_len)) return CC1D_ERR_SHAPE;
+    if (p->cu_seqlens == nullptr || p->states == nullptr || (p->x == nullptr && p->total_tokens > 0))
+        return CC1D_ERR_NULL_POINTER;
+    return launch_varlen_states(*p, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,468 @@
+// cc1d_bwd.hip -- fused backward kernels for gfx950.
+//
+// Semantics (src/causal_conv1d_mojo/bwd_full_cpu/kernel.mojo:25-314):
+//   dpre[t] = dout[t] * silu'(pre[t]) (or dout[t] without SiLU); 0 for t
+//             outside [0, L) and where seq_idx[t] < 0; pre is recomputed
+//             exactly as in the forward.
+//   dx[t]   = sum_k w[W-1-k] * dpre[t+k], tap k kept when seq_idx[t+k] == seq_idx[t]
+//   dw[k]  += sum_t dpre[t] * xx(t+k-(W-1)), same gate as the forward
+//   db     += sum_t dpre[t]
+//   dinit[i] = sum_{k<=i} w[k] * dpre[i-k]   (i < W-1)
+// dweight/dbias are reduced in fp32: per lane, across the wavefront
+// (ds_bpermute butterfly), across the block (LDS) and finally one fp32
+// atomic add per (block, tap) into the caller's zeroed accumulator.
+//
+// Kernels
+//   bwd_rows_vec -- channel-first rows, same lane layout as fwd_rows_vec.
+//                   All wavefronts of a block work on the same channel (its
+//                   batches / segments), so the weight-gradient partials of a
+//                   channel meet in LDS before touching global memory.
+//   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
+#include "cc1d_internal.hpp"
+
+namespace cc1d {
+
+struct BwdArgs {
+    cc1d_bwd_params p;
+    int64_t nseg;     // segments / chunks per row
+    int64_t n_items;  // rows_vec: items per channel (B * nseg); generic: threads
+    int64_t groups;   // rows_vec: blocks per channel
+    int64_t chunk;    // generic: time steps per thread
+};
+
+template <typename T, int W, int VPT, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
+    constexpr int EPV = elems16<T>::value;
+    constexpr int H = W - 1;
+    constexpr int SEG = 64 * VPT * EPV;
+    static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
+    const cc1d_bwd_params& p = a.p;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t c = uniform((int64_t)blockIdx.x / a.groups);
+    const int64_t it = uniform(((int64_t)blockIdx.x - c * a.groups) * 4 + wave);
+    const int64_t L = p.seqlen;
+    __shared__ float red[4][W + 1];
+
+    float w[W];
+    const T* __restrict__ wr = static_cast<const T*>(p.weight) + c * p.weight_stride[0];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = ld(wr, k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
+
+    float pw[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
+    float pb = 0.0f;
+
+    if (it < a.n_items) {
+        const int64_t b = it / a.nseg;
+        const int64_t t0 = (it - b * a.nseg) * SEG;
+        const int64_t tn = t0 + SEG;  // first position of the next segment
+        const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+        const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
+        T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
+
+        u32x4 v[VPT], gv[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            v[j] = (t < L) ? vload(xr + t) : vzero();
+            gv[j] = (t < L) ? vload(gr + t) : vzero();
+        }
+        u32x4 h = vzero(), xn = vzero(), gn = vzero();
+        if (lane == 0 && t0 > 0) h = vload(xr - EPV + t0);
+        if (lane == 63 && tn < L) {
+            xn = vload(xr + tn);
+            gn = vload(gr + tn);
+        }
+
+        int32_t id[VPT][EPV];
+        int32_t hid[H], nid[H];
+        if constexpr (SEQ) {
+            const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) {
+                const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+#pragma unroll
+                for (int q = 0; q < EPV / 4; ++q) {
+                    const u32x4 s = (t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                                            : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                hid[i] = (lane == 0 && t0 - H + i >= 0) ? sr[t0 - H + i] : -1;
+                nid[i] = (lane == 63 && tn + i < L) ? sr[tn + i] : -1;
+            }
+        }
+
+        const bool use_init = p.initial_states != nullptr && t0 == 0 && lane == 0;
+        float hinit[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            hinit[i] = 0.0f;
+            if (use_init)
+                hinit[i] = ld(static_cast<const T*>(p.initial_states),
+                              b * p.initial_states_stride[0] + c * p.initial_states_stride[1] +
+                                  i * p.initial_states_stride[2]);
+        }
+
+        // ---- dpre for the owned positions + dweight/dbias partials ----
+        constexpr int D0 = ((EPV - H) * (int)sizeof(T)) / 4;
+        const int prev_lane = (lane + 63) & 63;
+        const int next_lane = (lane + 1) & 63;
+        float dp[VPT][EPV];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            u32x4 pv = vzero();
+#pragma unroll
+            for (int d = D0; d < 4; ++d) {
+                const uint32_t send = (lane == 63) ? (j > 0 ? v[j > 0 ? j - 1 : 0][d] : 0u) : v[j][d];
+                pv[d] = lane_get(send, prev_lane);
+            }
+            if (j == 0 && lane == 0) pv = h;
+            float win[H + EPV];
+#pragma unroll
+            for (int i = 0; i < H; ++i) win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
+#pragma unroll
+            for (int i = 0; i < EPV; ++i) win[H + i] = vget<T>(v[j], i);
+            int32_t sw[H + EPV];
+            if constexpr (SEQ) {
+#pragma unroll
+                for (int i = 0; i < H; ++i) {
+                    const int32_t send = (lane == 63) ? (j > 0 ? id[j > 0 ? j - 1 : 0][EPV - H + i] : -1)
+                                                      : id[j][EPV - H + i];
+                    const int32_t r = lane_get(send, prev_lane);
+                    sw[i] = (j == 0 && lane == 0) ? hid[i] : r;
+                }
+#pragma unroll
+                for (int i = 0; i < EPV; ++i) sw[H + i] = id[j][i];
+            }
+#pragma unroll
+            for (int i = 0; i < EPV; ++i) {
+                const float g = vget<T>(gv[j], i);
+                float d = g;
+                if constexpr (SILU) {
+                    float pre = bias;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) {
+                        if constexpr (SEQ) {
+                            if (sw[i + k] == sw[H + i]) pre = __builtin_fmaf(w[k], win[i + k], pre);
+                        } else {
+                            pre = __builtin_fmaf(w[k], win[i + k], pre);
+                        }
+                    }
+                    d = g * silu_grad(pre);
+                }
+                if (t >= L) d = 0.0f;
+                if constexpr (SEQ) {
+                    if (sw[H + i] < 0) d = 0.0f;
+                }
+                dp[j][i] = d;
+                pb += d;
+#pragma unroll
+                for (int k = 0; k < W; ++k) {
+                    if constexpr (SEQ) {
+                        if (sw[i + k] == sw[H + i]) pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
+                    } else {
+                        pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
+                    }
+                }
+            }
+        }
+
+        // ---- dpre of the first H positions of the next segment (used by lane 63) ----
+        float dn[H];
+        {
+            float xw[2 * H];
+            int32_t iw[2 * H];
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                xw[i] = vget<T>(v[VPT - 1], EPV - H + i);
+                xw[H + i] = vget<T>(xn, i);
+                if constexpr (SEQ) {
+                    iw[i] = id[VPT - 1][EPV - H + i];
+                    iw[H + i] = nid[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float g = vget<T>(gn, i);
+                float d = g;
+                if constexpr (SILU) {
+                    float pre = bias;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) {
+                        if constexpr (SEQ) {
+                            if (iw[i + k] == iw[H + i]) pre = __builtin_fmaf(w[k], xw[i + k], pre);
+                        } else {
+                            pre = __builtin_fmaf(w[k], xw[i + k], pre);
+                        }
+                    }
+                    d = g * silu_grad(pre);
+                }
+                if (tn + i >= L) d = 0.0f;
+                if constexpr (SEQ) {
+                    if (iw[H + i] < 0) d = 0.0f;
+                }
+                dn[i] = d;
+            }
+        }
+
+        // ---- dx ----
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            float de[EPV + H];
+            int32_t ie[EPV + H];
+#pragma unroll
+            for (int i = 0; i < EPV; ++i) {
+                de[i] = dp[j][i];
+                if constexpr (SEQ) ie[i] = id[j][i];
+            }
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float send = (lane == 0) ? (j + 1 < VPT ? dp[j + 1 < VPT ? j + 1 : 0][i] : 0.0f) : dp[j][i];
+                const float r = lane_get(send, next_lane);
+                de[EPV + i] = (lane == 63 && j == VPT - 1) ? dn[i] : r;
+                if constexpr (SEQ) {
+                    const int32_t s = (lane == 0) ? (j + 1 < VPT ? id[j + 1 < VPT ? j + 1 : 0][i] : -1) : id[j][i];
+                    const int32_t ri = lane_get(s, next_lane);
+                    ie[EPV + i] = (lane == 63 && j == VPT - 1) ? nid[i] : ri;
+                }
+            }
+            float o[EPV];
+#pragma unroll
+            for (int i = 0; i < EPV; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < W; ++k) {
+                    if constexpr (SEQ) {
+                        if (ie[i + k] == ie[i]) acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
+                    } else {
+                        acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
+                    }
+                }
+                o[i] = acc;
+            }
+            // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
+            // here, so the W-1 tail positions are the end of the last vector.
+            if (p.dfinal_states != nullptr && t + EPV == L) {
+                const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
+                               c * p.dfinal_states_stride[1];
+#pragma unroll
+                for (int i = EPV - H; i < EPV; ++i)
+                    o[i] = round_to<T>(o[i]) + ld(dfs, (H - EPV + i) * p.dfinal_states_stride[2]);
+            }
+            if (t < L) vstore(dxr + t, vpack<T>(o));
+        }
+
+        // ---- dinitial_states (bwd_full_cpu/kernel.mojo:210-219) ----
+        if (p.dinitial_states != nullptr && t0 == 0 && lane == 0) {
+            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
+                    c * p.dinitial_states_stride[1];
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], dp[0][i - k], acc);
+                st(di, i * p.dinitial_states_stride[2], acc);
+            }
+        }
+    }
+
+    // ---- weight / bias gradient reduction ----
+#pragma unroll
+    for (int k = 0; k < W; ++k) pw[k] = wave_sum(pw[k]);
+    pb = wave_sum(pb);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < W; ++k) red[wave][k] = pw[k];
+        red[wave][W] = pb;
+    }
+    __syncthreads();
+    if (threadIdx.x <= W) {
+        const int k = threadIdx.x;
+        const float s = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
+        if (k < W)
+            unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], s);
+        else if (p.dbias_acc != nullptr)
+            unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, s);
+    }
+}
+
+template <typename T, int W, bool SILU>
+__global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
+    constexpr int H = W - 1;
+    const cc1d_bwd_params& p = a.p;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n_items) return;
+    const int64_t c = idx % p.dim;
+    const int64_t rest = idx / p.dim;
+    const int64_t ch = rest % a.nseg;
+    const int64_t b = rest / a.nseg;
+    const int64_t L = p.seqlen;
+    const int64_t t0 = ch * a.chunk;
+    const int64_t t1 = (t0 + a.chunk < L) ? t0 + a.chunk : L;
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
+    T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
+    const int32_t* sr = p.seq_idx ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
+    const T* ir = p.initial_states ? static_cast<const T*>(p.initial_states) + b * p.initial_states_stride[0] +
+                                         c * p.initial_states_stride[1]
+                                   : nullptr;
+
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        w[k] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
+
+    // Windows over positions s-H..s: x values, seq ids, dpre values.
+    float xw[W], dw[W];
+    int32_t iw[W];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        const int64_t s = t0 - H + i;
+        if (s >= 0) xw[i] = ld(xr, s * p.x_stride[2]);
+        else xw[i] = ir ? ld(ir, (s + H) * p.initial_states_stride[2]) : 0.0f;
+        iw[i] = (sr != nullptr && s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
+        dw[i] = 0.0f;
+    }
+    float pw[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
+    float pb = 0.0f;
+    float dfirst[H];
+#pragma unroll
+    for (int i = 0; i < H; ++i) dfirst[i] = 0.0f;
+
+    const int64_t m = (H < L) ? H : L;  // dfinal tail length
+    for (int64_t s = t0; s < t1 + H; ++s) {
+        const bool in = s < L;
+        xw[H] = in ? ld(xr, s * p.x_stride[2]) : 0.0f;
+        iw[H] = (in && sr != nullptr) ? sr[s * p.seq_idx_stride[1]] : -1;
+        float d = 0.0f;
+        if (in) {
+            const float g = ld(gr, s * p.dout_stride[2]);
+            d = g;
+            if (SILU) {
+                float pre = bias;
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (sr == nullptr || iw[k] == iw[H]) pre = __builtin_fmaf(w[k], xw[k], pre);
+                d = g * silu_grad(pre);
+            }
+            if (sr != nullptr && iw[H] < 0) d = 0.0f;
+        }
+        dw[H] = d;
+        if (s < t1) {
+            pb += d;
+#pragma unroll
+            for (int k = 0; k < W; ++k)
+                if (sr == nullptr || iw[k] == iw[H]) pw[k] = __builtin_fmaf(d, xw[k], pw[k]);
+#pragma unroll
+            for (int i = 0; i < H; ++i)
+                if (s == i) dfirst[i] = d;
+        }
+        const int64_t q = s - H;
+        if (q >= t0) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < W; ++k)
+                if (sr == nullptr || iw[k] == iw[0]) acc = __builtin_fmaf(w[W - 1 - k], dw[k], acc);
+            if (p.dfinal_states != nullptr && q >= L - m)
+                acc = round_to<T>(acc) + ld(static_cast<const T*>(p.dfinal_states),
+                                            b * p.dfinal_states_stride[0] + c * p.dfinal_states_stride[1] +
+                                                (q - L + H) * p.dfinal_states_stride[2]);
+            st(dxr, q * p.dx_stride[2], acc);
+        }
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            xw[i] = xw[i + 1];
+            iw[i] = iw[i + 1];
+            dw[i] = dw[i + 1];
+        }
+    }
+    if (p.dinitial_states != nullptr && t0 == 0) {
+        T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] + c * p.dinitial_states_stride[1];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], dfirst[i - k], acc);
+            st(di, i * p.dinitial_states_stride[2], acc);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], pw[k]);
+    if (p.dbias_acc != nullptr) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, pb);
+}
+
+namespace {
+
+template <typename T>
+bool rows_vec_ok(const cc1d_bwd_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    if (p.width - 1 > EPV) return false;
+    if (p.x_stride[2] != 1 || p.dout_stride[2] != 1 || p.dx_stride[2] != 1) return false;
+    if (p.seqlen % EPV != 0) return false;
+    if (!aligned16(p.x) || !aligned16(p.dout) || !aligned16(p.dx)) return false;
+    if (p.x_stride[0] % EPV || p.x_stride[1] % EPV || p.dout_stride[0] % EPV || p.dout_stride[1] % EPV ||
+        p.dx_stride[0] % EPV || p.dx_stride[1] % EPV)
+        return false;
+    if (p.seq_idx != nullptr &&
+        (p.seq_idx_stride[1] != 1 || p.seq_idx_stride[0] % 4 != 0 || !aligned16(p.seq_idx)))
+        return false;
+    return true;
+}
+
+}  // namespace
+
+int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
+    return with_dtype(p.dtype, [&](auto tag) {
+        using T = decltype(tag);
+        constexpr int64_t EPV = elems16<T>::value;
+        return with_width(p.width, [&](auto wc) {
+            constexpr int W = decltype(wc)::value;
+            return with_flag(p.apply_silu != 0, [&](auto sc) {
+                constexpr bool SILU = decltype(sc)::value;
+                BwdArgs a;
+                a.p = p;
+                a.chunk = 0;
+                a.groups = 0;
+                if constexpr (W - 1 <= EPV) {
+                    if (rows_vec_ok<T>(p)) {
+                        const int64_t nvec = p.seqlen / EPV;
+                        const int64_t per = ceil_div(nvec, 64);
+                        const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+                        a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
+                        a.n_items = p.batch * a.nseg;
+                        a.groups = ceil_div(a.n_items, 4);
+                        const dim3 grid((unsigned)(p.dim * a.groups));
+                        return with_flag(p.seq_idx != nullptr, [&](auto qc) {
+                            constexpr bool SEQ = decltype(qc)::value;
+                            if (vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                            else if (vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                            else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                            return launch_status();
+                        });
+                    }
+                }
+                a.chunk = 64;
+                a.nseg = ceil_div(p.seqlen, a.chunk);
+                a.n_items = p.batch * p.dim * a.nseg;
+                const dim3 grid((unsigned)ceil_div(a.n_items, 256));
+                bwd_generic<T, W, SILU><<<grid, 256, 0, stream>>>(a);
+                return launch_status();
+            });
+        });
+    });
+}
+
+}  // namespace cc1d

@@ -1,0 +1,145 @@
+// cc1d_device.hpp -- device helpers shared by the gfx950 causal conv1d kernels.
+//
+// Storage types are tag structs around the raw bits so that every conversion
+// is explicit: bf16/fp16 widen exactly to fp32 and narrow with one
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32 / v_cvt_f16_f32 on
+// gfx950). Rows move through HBM as 16-byte vectors (global_load_dwordx4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cc1d {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct f16 { uint16_t bits; };
+struct bf16 { uint16_t bits; };
+
+template <typename T> struct elems16 { static constexpr int value = 16 / (int)sizeof(T); };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return __uint_as_float((uint32_t)v.bits << 16); }
+__device__ __forceinline__ float to_f32(f16 v) { return (float)__builtin_bit_cast(_Float16, v.bits); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) {
+    return bf16{__builtin_bit_cast(uint16_t, (__bf16)v)};
+}
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) {
+    return f16{__builtin_bit_cast(uint16_t, (_Float16)v)};
+}
+
+// Round-trip through the storage dtype (what a store followed by a load gives).
+template <typename T> __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// Element e (compile-time after unrolling) of a 16-byte vector, widened to fp32.
+template <typename T> __device__ __forceinline__ float vget(const u32x4& v, int e);
+template <> __device__ __forceinline__ float vget<float>(const u32x4& v, int e) { return __uint_as_float(v[e]); }
+template <> __device__ __forceinline__ float vget<bf16>(const u32x4& v, int e) {
+    const uint32_t d = v[e >> 1];
+    return (e & 1) ? __uint_as_float(d & 0xffff0000u) : __uint_as_float(d << 16);
+}
+template <> __device__ __forceinline__ float vget<f16>(const u32x4& v, int e) {
+    const uint32_t d = v[e >> 1];
+    const uint16_t h = (e & 1) ? (uint16_t)(d >> 16) : (uint16_t)(d & 0xffffu);
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Pack EPV fp32 values into one 16-byte vector of T (one RNE rounding each).
+template <typename T> __device__ __forceinline__ u32x4 vpack(const float* f);
+template <> __device__ __forceinline__ u32x4 vpack<float>(const float* f) {
+    u32x4 r;
+    r[0] = __float_as_uint(f[0]); r[1] = __float_as_uint(f[1]);
+    r[2] = __float_as_uint(f[2]); r[3] = __float_as_uint(f[3]);
+    return r;
+}
+template <> __device__ __forceinline__ u32x4 vpack<bf16>(const float* f) {
+    u32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        r[d] = (uint32_t)from_f32<bf16>(f[2 * d]).bits | ((uint32_t)from_f32<bf16>(f[2 * d + 1]).bits << 16);
+    return r;
+}
+template <> __device__ __forceinline__ u32x4 vpack<f16>(const float* f) {
+    u32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        r[d] = (uint32_t)from_f32<f16>(f[2 * d]).bits | ((uint32_t)from_f32<f16>(f[2 * d + 1]).bits << 16);
+    return r;
+}
+
+__device__ __forceinline__ u32x4 vzero() { u32x4 z = {0u, 0u, 0u, 0u}; return z; }
+
+template <typename T> __device__ __forceinline__ u32x4 vload(const T* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+template <typename T> __device__ __forceinline__ void vstore(T* p, const u32x4& v) {
+    *reinterpret_cast<u32x4*>(p) = v;
+}
+
+template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
+template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
+
+// SiLU = x * sigmoid(x), as x * rcp(1 + exp(-x)) in fp32.
+__device__ __forceinline__ float silu(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
+
+// d silu / d x = s * (1 + x * (1 - s)), s = sigmoid(x).
+__device__ __forceinline__ float silu_grad(float x) {
+    const float s = __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    return s * (1.0f + x * (1.0f - s));
+}
+
+// Causal taps: bias + sum_k w[k] * win[k], fp32 fma in k order. The forward
+// and the decode update both use this, so a decode loop reproduces the full
+// forward bit for bit.
+template <int W>
+__device__ __forceinline__ float conv_taps(float bias, const float* w, const float* win) {
+    float acc = bias;
+#pragma unroll
+    for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], win[k], acc);
+    return acc;
+}
+
+// As conv_taps, keeping tap k only when ids[k] equals the current id ids[W-1].
+template <int W>
+__device__ __forceinline__ float conv_taps_gated(float bias, const float* w, const float* win,
+                                                 const int32_t* ids) {
+    float acc = bias;
+    const int32_t cur = ids[W - 1];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        if (ids[k] == cur) acc = __builtin_fmaf(w[k], win[k], acc);
+    return acc;
+}
+
+// Value of `v` held by lane `src` of this wavefront (ds_bpermute_b32).
+__device__ __forceinline__ uint32_t lane_get(uint32_t v, int src) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)v);
+}
+__device__ __forceinline__ float lane_get(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ int32_t lane_get(int32_t v, int src) {
+    return __builtin_amdgcn_ds_bpermute(src << 2, v);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += lane_get(v, lane ^ m);
+    return v;
+}
+
+// Wavefront-uniform value (lets the compiler keep it in an SGPR).
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+}  // namespace cc1d

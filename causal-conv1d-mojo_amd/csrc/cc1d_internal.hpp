@@ -1,0 +1,60 @@
+// cc1d_internal.hpp -- host-side glue shared by the launcher translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "cc1d.h"
+#include "cc1d_device.hpp"
+
+namespace cc1d {
+
+// Launchers (one per kernel family). The arguments were validated by the C
+// ABI layer; each returns a cc1d_status.
+int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream);
+int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream);
+int launch_update(const cc1d_update_params& p, hipStream_t stream);
+int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream);
+
+// Compile-time dispatch over the runtime dtype code / width / flags.
+template <typename F> int with_dtype(int dtype, F&& f) {
+    switch (dtype) {
+    case CC1D_DTYPE_FP16: return f(f16{});
+    case CC1D_DTYPE_BF16: return f(bf16{});
+    case CC1D_DTYPE_FP32: return f(float{});
+    default: return CC1D_ERR_DTYPE;
+    }
+}
+
+template <typename F> int with_width(int64_t width, F&& f) {
+    switch (width) {
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 3: return f(std::integral_constant<int, 3>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 5: return f(std::integral_constant<int, 5>{});
+    case 6: return f(std::integral_constant<int, 6>{});
+    case 7: return f(std::integral_constant<int, 7>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    case 9: return f(std::integral_constant<int, 9>{});
+    default: return CC1D_ERR_WIDTH;
+    }
+}
+
+template <typename F> int with_flag(bool flag, F&& f) {
+    return flag ? f(std::true_type{}) : f(std::false_type{});
+}
+
+inline int launch_status() {
+    return hipGetLastError() == hipSuccess ? CC1D_OK : CC1D_ERR_LAUNCH;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Zero-fills a (n0, n1, n2) strided tensor of `esize`-byte elements.
+int launch_zero3(void* ptr, int esize, int64_t n0, int64_t n1, int64_t n2,
+                 const int64_t* stride, hipStream_t stream);
+
+}  // namespace cc1d

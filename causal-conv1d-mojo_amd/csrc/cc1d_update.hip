@@ -1,0 +1,209 @@
+// cc1d_update.hip -- decode (single-token / short-burst) update kernels.
+//
+// Semantics (src/causal_conv1d_mojo/update_cpu/kernel.mojo:49-141):
+//   full = cat(history, x[b,c,0:seqlen]) where history is the W-1 values
+//   before the write head: state[-(W-1):] (linear) or
+//   state[(cs - (W-1) + j) mod S] with cs = cache_seqlens[b] mod S (circular).
+//   out[i] = act(bias + sum_k w[k] * full[i+k])
+//   linear:   state <- last S values of cat(state, x)
+//   circular: state[(cs + i) mod S] <- x[i]
+//   conv_state_indices redirect the state row; a negative (padding) or
+//   out-of-pool index zeroes out[b] and leaves the pool untouched.
+//
+// Kernels
+//   update_vec1    -- linear mode, one token, S == W-1, channel-contiguous x /
+//                     out and contiguous state rows: a lane owns EPV adjacent
+//                     channels, so x, out, weight and the (EPV x S) state
+//                     block move as 16-byte vectors.
+//   update_generic -- everything else; one thread per (b, c).
+// Both use the forward's tap loop (fma in k order, then SiLU), so a decode
+// loop reproduces the full forward bit for bit.
+#include "cc1d_internal.hpp"
+
+namespace cc1d {
+
+struct UpdArgs {
+    cc1d_update_params p;
+    int64_t n_items;
+    int64_t ngroups;  // channel groups per batch row (vec1)
+};
+
+__device__ __forceinline__ int64_t state_row(const cc1d_update_params& p, int64_t b) {
+    if (p.conv_state_indices == nullptr) return b;
+    const int64_t r = p.conv_state_indices[b];
+    return (r < 0 || r >= p.state_rows) ? -1 : r;
+}
+
+template <typename T, int W, bool SILU, bool CIRC>
+__global__ void __launch_bounds__(256) update_generic(const UpdArgs a) {
+    constexpr int H = W - 1;
+    const cc1d_update_params& p = a.p;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n_items) return;
+    const int64_t c = idx % p.dim;
+    const int64_t b = idx / p.dim;
+    const int64_t Ls = p.seqlen;
+    const int64_t S = p.state_len;
+    T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+    const int64_t row = state_row(p, b);
+    if (row < 0) {
+        for (int64_t i = 0; i < Ls; ++i) st(orow, i * p.out_stride[2], 0.0f);
+        return;
+    }
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+    T* __restrict__ sr = static_cast<T*>(p.conv_state) + row * p.conv_state_stride[0] + c * p.conv_state_stride[1];
+    const int64_t ss = p.conv_state_stride[2];
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        w[k] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
+
+    float win[W];
+    int64_t head = 0;
+    if constexpr (CIRC) {
+        int64_t cs = (int64_t)p.cache_seqlens[b] % S;
+        if (cs < 0) cs += S;  // floored modulo (torch.remainder)
+        head = cs - H;
+        if (head < 0) head += S;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            win[i] = ld(sr, head * ss);
+            if (++head >= S) head -= S;
+        }
+    } else {
+        // shift left by Ls, keeping the W-1 history values in registers
+        for (int64_t i = 0; i < S - Ls - H; ++i) sr[i * ss] = sr[(i + Ls) * ss];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const T v = sr[(S - H + i) * ss];
+            const int64_t wi = S - Ls - H + i;
+            if (wi >= 0) sr[wi * ss] = v;
+            win[i] = to_f32(v);
+        }
+    }
+    for (int64_t i = 0; i < Ls; ++i) {
+        const T xv = xr[i * p.x_stride[2]];
+        if constexpr (CIRC) {
+            sr[head * ss] = xv;
+            if (++head >= S) head -= S;
+        } else {
+            const int64_t wi = S - Ls + i;
+            if (wi >= 0) sr[wi * ss] = xv;
+        }
+        win[H] = to_f32(xv);
+        float acc = conv_taps<W>(bias, w, win);
+        if constexpr (SILU) acc = silu(acc);
+        st(orow, i * p.out_stride[2], acc);
+#pragma unroll
+        for (int k = 0; k < H; ++k) win[k] = win[k + 1];
+    }
+}
+
+// Linear mode, seqlen 1, state_len == W-1. Lane -> (b, EPV channels).
+template <typename T, int W, bool SILU>
+__global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
+    constexpr int EPV = elems16<T>::value;
+    constexpr int H = W - 1;
+    constexpr int NV = H;  // 16-byte vectors in an (EPV x H) state block
+    const cc1d_update_params& p = a.p;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n_items) return;
+    const int64_t g = idx % a.ngroups;
+    const int64_t b = idx / a.ngroups;
+    const int64_t c0 = g * EPV;
+    T* __restrict__ op = static_cast<T*>(p.out) + b * p.out_stride[0] + c0;
+    const int64_t row = state_row(p, b);
+    if (row < 0) {
+        vstore(op, vzero());
+        return;
+    }
+    const u32x4 xv = vload(static_cast<const T*>(p.x) + b * p.x_stride[0] + c0);
+    T* __restrict__ sp = static_cast<T*>(p.conv_state) + row * p.conv_state_stride[0] + c0 * H;
+    u32x4 sv[NV];
+#pragma unroll
+    for (int n = 0; n < NV; ++n) sv[n] = vload(sp + n * EPV);
+    // contiguous (dim, W) weight: EPV*W values = W vectors
+    u32x4 wv[W];
+    const T* wp = static_cast<const T*>(p.weight) + c0 * W;
+#pragma unroll
+    for (int n = 0; n < W; ++n) wv[n] = vload(wp + n * EPV);
+    u32x4 bv = vzero();
+    if (p.bias) bv = vload(static_cast<const T*>(p.bias) + c0);
+
+    float o[EPV];
+    float ns[EPV * H];
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+        float win[W], w[W];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const int n = e * H + i;
+            win[i] = vget<T>(sv[n / EPV], n % EPV);
+        }
+        win[H] = vget<T>(xv, e);
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+            const int n = e * W + k;
+            w[k] = vget<T>(wv[n / EPV], n % EPV);
+        }
+        float acc = conv_taps<W>(vget<T>(bv, e), w, win);
+        if constexpr (SILU) acc = silu(acc);
+        o[e] = acc;
+#pragma unroll
+        for (int i = 0; i < H; ++i) ns[e * H + i] = win[i + 1];
+    }
+    vstore(op, vpack<T>(o));
+#pragma unroll
+    for (int n = 0; n < NV; ++n) vstore(sp + n * EPV, vpack<T>(ns + n * EPV));
+}
+
+namespace {
+
+template <typename T>
+bool vec1_ok(const cc1d_update_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    const int64_t H = p.width - 1;
+    if (p.cache_seqlens != nullptr || p.seqlen != 1 || p.state_len != H) return false;
+    if (p.dim % EPV != 0) return false;
+    if (p.x_stride[1] != 1 || p.out_stride[1] != 1) return false;
+    if (p.x_stride[0] % EPV || p.out_stride[0] % EPV) return false;
+    if (p.conv_state_stride[2] != 1 || p.conv_state_stride[1] != H || p.conv_state_stride[0] % EPV) return false;
+    if (p.weight_stride[1] != 1 || p.weight_stride[0] != p.width) return false;
+    if (p.bias != nullptr && (p.bias_stride != 1 || !aligned16(p.bias))) return false;
+    if (!aligned16(p.x) || !aligned16(p.out) || !aligned16(p.conv_state) || !aligned16(p.weight)) return false;
+    return true;
+}
+
+}  // namespace
+
+int launch_update(const cc1d_update_params& p, hipStream_t stream) {
+    return with_dtype(p.dtype, [&](auto tag) {
+        using T = decltype(tag);
+        constexpr int64_t EPV = elems16<T>::value;
+        return with_width(p.width, [&](auto wc) {
+            constexpr int W = decltype(wc)::value;
+            return with_flag(p.apply_silu != 0, [&](auto sc) {
+                constexpr bool SILU = decltype(sc)::value;
+                UpdArgs a;
+                a.p = p;
+                a.ngroups = 0;
+                if (vec1_ok<T>(p)) {
+                    a.ngroups = p.dim / EPV;
+                    a.n_items = p.batch * a.ngroups;
+                    update_vec1<T, W, SILU><<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
+                    return launch_status();
+                }
+                a.n_items = p.batch * p.dim;
+                const dim3 grid((unsigned)ceil_div(a.n_items, 256));
+                return with_flag(p.cache_seqlens != nullptr, [&](auto cc) {
+                    constexpr bool CIRC = decltype(cc)::value;
+                    update_generic<T, W, SILU, CIRC><<<grid, 256, 0, stream>>>(a);
+                    return launch_status();
+                });
+            });
+        });
+    });
+}
+
+}  // namespace cc1d

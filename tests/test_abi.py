@@ -1,0 +1,160 @@
+"""C-ABI checks that need no GPU.
+
+* ``libcc1d_amd.so`` loads and exports every function ``include/cc1d.h``
+  declares;
+* the ctypes structures of ``causal_conv1d_amd._lib`` have the size and
+  field offsets that gcc computes from the header;
+* argument validation returns the documented status codes before any HIP
+  call (NULL params, bad dtype / width / shape, mutually exclusive inputs,
+  short conv_state) and zero-size problems return CC1D_OK without work.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from causal_conv1d_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "cc1d.h"
+
+OK, ERR_NULL, ERR_DTYPE, ERR_WIDTH, ERR_SHAPE, ERR_EXCL, ERR_STATE = 0, 1, 2, 3, 4, 5, 6
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cc1d_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_bound_entry_points():
+    assert _declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (cc1d_\w+)$", out, re.M))
+    for name in _declared_functions():
+        assert name in exported, f"{name} not exported"
+        assert getattr(lib, name) is not None
+
+
+def test_abi_version_and_strerror(lib):
+    assert lib.cc1d_abi_version() == _lib.ABI_VERSION == 1
+    for code in range(0, 8):
+        msg = lib.cc1d_strerror(code).decode()
+        assert msg and msg != "unknown status"
+    assert lib.cc1d_strerror(99).decode() == "unknown status"
+
+
+STRUCTS = {
+    "cc1d_fwd_params": _lib.FwdParams,
+    "cc1d_bwd_params": _lib.BwdParams,
+    "cc1d_update_params": _lib.UpdateParams,
+    "cc1d_varlen_params": _lib.VarlenParams,
+}
+
+
+def test_struct_layout_matches_header(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "cc1d.h"', "int main(void) {"]
+    for cname, st in STRUCTS.items():
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _ in st._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for ln in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        s, f, v = ln.split()
+        got[(s, f)] = int(v)
+    for cname, st in STRUCTS.items():
+        assert got[(cname, "sizeof")] == ctypes.sizeof(st), cname
+        for fname, _ in st._fields_:
+            assert got[(cname, fname)] == getattr(st, fname).offset, f"{cname}.{fname}"
+
+
+def _fwd(**kw):
+    p = _lib.FwdParams()
+    p.batch, p.dim, p.seqlen, p.width, p.dtype = 1, 8, 16, 4, 1
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_fwd_validation_codes(lib):
+    call = lambda p: lib.cc1d_fwd(ctypes.byref(p), None)  # noqa: E731
+    assert lib.cc1d_fwd(None, None) == ERR_NULL
+    assert call(_fwd(dtype=3)) == ERR_DTYPE
+    assert call(_fwd(width=1)) == ERR_WIDTH
+    assert call(_fwd(width=10)) == ERR_WIDTH
+    assert call(_fwd(seqlen=-1)) == ERR_SHAPE
+    assert call(_fwd(seq_idx=16, initial_states=16)) == ERR_EXCL
+    assert call(_fwd(seq_idx=16, final_states_out=16)) == ERR_EXCL
+    assert call(_fwd()) == ERR_NULL  # x / weight / out missing
+    assert call(_fwd(batch=0)) == OK  # zero-size: nothing to do
+    assert call(_fwd(dim=0)) == OK
+    assert call(_fwd(seqlen=0)) == OK  # no final_states requested
+
+
+def test_bwd_validation_codes(lib):
+    def call(**kw):
+        p = _lib.BwdParams()
+        p.batch, p.dim, p.seqlen, p.width, p.dtype = 1, 8, 16, 4, 1
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return lib.cc1d_bwd(ctypes.byref(p), None)
+
+    assert lib.cc1d_bwd(None, None) == ERR_NULL
+    assert call(dtype=-1) == ERR_DTYPE
+    assert call(width=11) == ERR_WIDTH
+    assert call(seq_idx=16, initial_states=16, dinitial_states=16) == ERR_EXCL
+    assert call(seq_idx=16, dfinal_states=16) == ERR_EXCL
+    assert call(initial_states=16) == ERR_NULL  # dinitial_states missing
+    assert call() == ERR_NULL
+    assert call(batch=0) == OK
+    assert call(seqlen=0) == OK
+
+
+def test_update_validation_codes(lib):
+    def call(**kw):
+        p = _lib.UpdateParams()
+        p.batch, p.dim, p.seqlen, p.width, p.state_len, p.state_rows, p.dtype = 2, 8, 1, 4, 3, 2, 1
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return lib.cc1d_update(ctypes.byref(p), None)
+
+    assert lib.cc1d_update(None, None) == ERR_NULL
+    assert call(state_len=2) == ERR_STATE
+    assert call(state_rows=1) == ERR_SHAPE  # no indices: one row per batch entry
+    assert call(width=10) == ERR_WIDTH
+    assert call() == ERR_NULL
+    assert call(seqlen=0) == OK
+    assert call(batch=0, state_rows=0) == OK
+
+
+def test_varlen_validation_codes(lib):
+    def call(**kw):
+        p = _lib.VarlenParams()
+        p.total_tokens, p.dim, p.batch, p.state_len, p.dtype = 10, 8, 2, 3, 1
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return lib.cc1d_varlen_states(ctypes.byref(p), None)
+
+    assert lib.cc1d_varlen_states(None, None) == ERR_NULL
+    assert call(dtype=7) == ERR_DTYPE
+    assert call(state_len=-1) == ERR_SHAPE
+    assert call() == ERR_NULL
+    assert call(batch=0) == OK

@@ -1,0 +1,95 @@
+"""HIP graph capture of the ops (reference tests/test_cuda_graph.py:138-190).
+
+The entry points allocate nothing, synchronise nothing and issue no
+memsets, so forward, backward (with its accumulator zero-fill done by a
+kernel) and update can be captured. Each graph is replayed several times
+with eager work and synchronisations in between, and every replay is
+compared with an eager run on the same inputs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import causal_conv1d_amd as cc
+from _util import make_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _capture(fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def test_forward_capture_replay_matches_eager():
+    x, w, b, _ = make_inputs(2, 64, 2048, 4, dtype=torch.bfloat16, device=DEV)
+    out_buf = torch.empty_like(x)
+    g = _capture(lambda: out_buf.copy_(cc.causal_conv1d_fn(x, w, b, activation="silu")))
+    for i in range(4):
+        x.copy_(torch.randn_like(x))  # in-place input mutation between replays
+        g.replay()
+        torch.cuda.synchronize()
+        eager = cc.causal_conv1d_fn(x, w, b, activation="silu")
+        _ = (eager.float() * 2).sum().item()  # unrelated eager work + sync between replays
+        assert torch.equal(out_buf, eager), f"replay {i}"
+
+
+def test_backward_ops_capture_replay_matches_eager():
+    B, D, L, W = 4, 256, 2048, 4
+    x, w, b, _ = make_inputs(B, D, L, W, dtype=torch.bfloat16, device=DEV)
+    dout = torch.randn_like(x)
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, W, dtype=torch.float32, device=DEV)
+    db = torch.empty(D, dtype=torch.float32, device=DEV)
+    out = torch.empty_like(x)
+
+    def step():
+        torch.ops.causal_conv1d_amd._fwd_inplace(x, w, b, None, None, out, True, None)
+        dw.zero_()
+        db.zero_()
+        torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dx, dw, db, None, True)
+
+    g = _capture(step)
+    for i in range(4):
+        dout.copy_(torch.randn_like(dout))
+        g.replay()
+        torch.cuda.synchronize()
+        snap = [t.clone() for t in (out, dx, dw, db)]
+        step()
+        torch.cuda.synchronize()
+        for name, a, e in zip(("out", "dx", "dweight", "dbias"), snap, (out, dx, dw, db)):
+            assert torch.equal(a, e), f"replay {i}: {name}"
+
+
+def test_update_capture_replay_matches_eager():
+    B, D, W = 64, 512, 4
+    x, w, b, _ = make_inputs(B, D, 1, W, dtype=torch.bfloat16, device=DEV)
+    x = x[..., 0].contiguous()
+    pool = torch.randn(2 * B, D, W - 1, dtype=torch.bfloat16, device=DEV)
+    idx = torch.randperm(2 * B, device=DEV)[:B].to(torch.int32)
+    out_buf = torch.empty_like(x)
+    state = pool.clone()
+    g = _capture(lambda: out_buf.copy_(cc.causal_conv1d_update(x, state, w, b, activation="silu",
+                                                               conv_state_indices=idx)))
+    for i in range(4):
+        state.copy_(pool)
+        x.copy_(torch.randn_like(x))
+        g.replay()
+        torch.cuda.synchronize()
+        got_out, got_state = out_buf.clone(), state.clone()
+        state.copy_(pool)
+        eager = cc.causal_conv1d_update(x, state, w, b, activation="silu", conv_state_indices=idx)
+        torch.cuda.synchronize()
+        assert torch.equal(got_out, eager), f"replay {i}: out"
+        assert torch.equal(got_state, state), f"replay {i}: state"
