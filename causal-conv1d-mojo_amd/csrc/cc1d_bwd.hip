@@ -30,35 +30,19 @@ struct BwdArgs {
     int64_t chunk;    // generic: time steps per thread
 };
 
-template <typename T, int W, int VPT, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
+// One wavefront-segment of row (b, c): writes dx (and dinitial_states) and
+// adds this segment's weight/bias-gradient partials into pw / pb. FULL: the
+// whole segment lies inside the row.
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+__device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
+                                                 int32_t t0, const float* w, float bias, float* pw, float& pb) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int SEG = 64 * VPT * EPV;
     static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
-    const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t c = uniform((int64_t)blockIdx.x / a.groups);
-    const int64_t it = uniform(((int64_t)blockIdx.x - c * a.groups) * 4 + wave);
-    const int64_t L = p.seqlen;
-    __shared__ float red[4][W + 1];
-
-    float w[W];
-    const T* __restrict__ wr = static_cast<const T*>(p.weight) + c * p.weight_stride[0];
-#pragma unroll
-    for (int k = 0; k < W; ++k) w[k] = ld(wr, k * p.weight_stride[1]);
-    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
-
-    float pw[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
-    float pb = 0.0f;
-
-    if (it < a.n_items) {
-        const int64_t b = it / a.nseg;
-        const int64_t t0 = (it - b * a.nseg) * SEG;
-        const int64_t tn = t0 + SEG;  // first position of the next segment
+    const int32_t L = (int32_t)p.seqlen;
+    {
+        const int32_t tn = t0 + SEG;  // first position of the next segment
         const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
         const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
         T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
@@ -66,9 +50,9 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
         u32x4 v[VPT], gv[VPT];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
-            v[j] = (t < L) ? vload(xr + t) : vzero();
-            gv[j] = (t < L) ? vload(gr + t) : vzero();
+            const int32_t t = t0 + (j * 64 + lane) * EPV;
+            v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
+            gv[j] = (FULL || t < L) ? vload_nt(gr + t) : vzero();
         }
         u32x4 h = vzero(), xn = vzero(), gn = vzero();
         if (lane == 0 && t0 > 0) h = vload(xr - EPV + t0);
@@ -83,10 +67,10 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
             const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
 #pragma unroll
             for (int j = 0; j < VPT; ++j) {
-                const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+                const int32_t t = t0 + (j * 64 + lane) * EPV;
 #pragma unroll
                 for (int q = 0; q < EPV / 4; ++q) {
-                    const u32x4 s = (t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                    const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
                                             : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
 #pragma unroll
                     for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
@@ -117,7 +101,7 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
         float dp[VPT][EPV];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            const int32_t t = t0 + (j * 64 + lane) * EPV;
             u32x4 pv = vzero();
 #pragma unroll
             for (int d = D0; d < 4; ++d) {
@@ -158,7 +142,7 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
                     }
                     d = g * silu_grad(pre);
                 }
-                if (t >= L) d = 0.0f;
+                if (!FULL && t >= L) d = 0.0f;
                 if constexpr (SEQ) {
                     if (sw[H + i] < 0) d = 0.0f;
                 }
@@ -216,7 +200,7 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
         // ---- dx ----
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            const int32_t t = t0 + (j * 64 + lane) * EPV;
             float de[EPV + H];
             int32_t ie[EPV + H];
 #pragma unroll
@@ -258,7 +242,7 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
                 for (int i = EPV - H; i < EPV; ++i)
                     o[i] = round_to<T>(o[i]) + ld(dfs, (H - EPV + i) * p.dfinal_states_stride[2]);
             }
-            if (t < L) vstore(dxr + t, vpack<T>(o));
+            if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
         }
 
         // ---- dinitial_states (bwd_full_cpu/kernel.mojo:210-219) ----
@@ -273,6 +257,42 @@ __global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
                 st(di, i * p.dinitial_states_stride[2], acc);
             }
         }
+    }
+}
+
+// Block = one channel c and four (batch, segment) items of it, so the
+// weight-gradient partials of a channel meet in LDS before one fp32 atomic
+// add per tap. All index arithmetic is 32-bit (the launcher checks ranges).
+template <typename T, int W, int VPT, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
+    constexpr int SEG = 64 * VPT * elems16<T>::value;
+    const cc1d_bwd_params& p = a.p;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t groups = (uint32_t)a.groups;
+    const uint32_t c = uniform32(blockIdx.x / groups);
+    const uint32_t it = uniform32((blockIdx.x - c * groups) * 4u + wave);
+    __shared__ float red[4][W + 1];
+
+    float w[W];
+    const T* __restrict__ wr = static_cast<const T*>(p.weight) + (int64_t)c * p.weight_stride[0];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = ld(wr, k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), (int64_t)c * p.bias_stride) : 0.0f;
+
+    float pw[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
+    float pb = 0.0f;
+
+    if (it < (uint32_t)a.n_items) {
+        const uint32_t nseg = (uint32_t)a.nseg;
+        const uint32_t b = it / nseg;
+        const int32_t t0 = (int32_t)((it - b * nseg) * SEG);
+        if (t0 + SEG <= (int32_t)p.seqlen)
+            bwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0, w, bias, pw, pb);
+        else
+            bwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0, w, bias, pw, pb);
     }
 
     // ---- weight / bias gradient reduction ----
@@ -419,6 +439,10 @@ bool rows_vec_ok(const cc1d_bwd_params& p) {
     if (p.seq_idx != nullptr &&
         (p.seq_idx_stride[1] != 1 || p.seq_idx_stride[0] % 4 != 0 || !aligned16(p.seq_idx)))
         return false;
+    // 32-bit index arithmetic: positions, blocks and items must fit
+    if (p.seqlen + 64 * 4 * EPV >= ((int64_t)1 << 31)) return false;
+    if (p.batch * ceil_div(p.seqlen, 64 * EPV) + 4 >= ((int64_t)1 << 31)) return false;
+    if (p.dim * (p.batch * ceil_div(p.seqlen, 64 * EPV) + 4) >= ((int64_t)1 << 31)) return false;
     return true;
 }
 

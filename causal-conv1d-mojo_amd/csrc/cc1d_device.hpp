@@ -79,6 +79,16 @@ template <typename T> __device__ __forceinline__ void vstore(T* p, const u32x4& 
     *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// Streaming (non-temporal) 16-byte accesses for data touched exactly once:
+// global_load/store_dwordx4 ... nt, so the stream does not displace reused
+// lines (weights, seq_idx, halos) from L2 / the Infinity Cache.
+template <typename T> __device__ __forceinline__ u32x4 vload_nt(const T* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+template <typename T> __device__ __forceinline__ void vstore_nt(T* p, const u32x4& v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
 template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 
@@ -136,6 +146,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Wavefront-uniform value (lets the compiler keep it in an SGPR).
+__device__ __forceinline__ uint32_t uniform32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int64_t uniform(int64_t v) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));

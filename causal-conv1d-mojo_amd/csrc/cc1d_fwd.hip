@@ -33,29 +33,22 @@ struct FwdArgs {
     int64_t ngroups;  // channel groups (cols)
 };
 
-template <typename T, int W, int VPT, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
+// One wavefront-segment of one row. FULL: the whole segment lies inside the
+// row (no per-vector bounds checks).
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+__device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int lane, int64_t b, int64_t c,
+                                                 int32_t t0) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
-    constexpr int SEG = 64 * VPT * EPV;
-    static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
-    const cc1d_fwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const int64_t item = uniform((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (item >= a.n_items) return;
-    const int64_t row = item / a.nseg;
-    const int64_t t0 = (item - row * a.nseg) * SEG;
-    const int64_t b = row / p.dim;
-    const int64_t c = row - b * p.dim;
-    const int64_t L = p.seqlen;
+    const int32_t L = (int32_t)p.seqlen;
     const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
     T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
 
     u32x4 v[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
-        v[j] = (t < L) ? vload(xr + t) : vzero();
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
+        v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
     }
     u32x4 h = vzero();
     if (lane == 0 && t0 > 0) h = vload(xr - EPV + t0);
@@ -66,11 +59,11 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
         const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+            const int32_t t = t0 + (j * 64 + lane) * EPV;
 #pragma unroll
             for (int q = 0; q < EPV / 4; ++q) {
-                const u32x4 s = (t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
-                                        : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+                const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                                                : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
             }
@@ -101,7 +94,7 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
     const int prev_lane = (lane + 63) & 63;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t t = t0 + (int64_t)(j * 64 + lane) * EPV;
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
         u32x4 pv = vzero();
 #pragma unroll
         for (int d = D0; d < 4; ++d) {
@@ -140,7 +133,7 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
             }
             o[i] = acc;
         }
-        if (t < L) vstore(orow + t, vpack<T>(o));
+        if (FULL || t < L) vstore_nt(orow + t, vpack<T>(o));
 
         // final_states (_fn.py:31-50): the lane holding position L-1 owns the
         // last W-1 columns (L % EPV == 0 on this path, so they are win[EPV..]).
@@ -152,6 +145,26 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
                 st(fs, i * p.final_states_stride[2], (L - H + i >= 0) ? win[EPV + i] : 0.0f);
         }
     }
+}
+
+// Item = (row, segment) with row = b * dim + c; four wavefronts per block take
+// four consecutive items, i.e. adjacent segments of a row or adjacent rows.
+// All index arithmetic is 32-bit (the launcher checks the ranges).
+template <typename T, int W, int VPT, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
+    constexpr int SEG = 64 * VPT * elems16<T>::value;
+    const cc1d_fwd_params& p = a.p;
+    const int lane = threadIdx.x & 63;
+    const uint32_t item = uniform32(blockIdx.x * 4u + (threadIdx.x >> 6));
+    if (item >= (uint32_t)a.n_items) return;
+    const uint32_t nseg = (uint32_t)a.nseg;
+    const uint32_t row = item / nseg;
+    const int32_t t0 = (int32_t)((item - row * nseg) * SEG);
+    const uint32_t dim = (uint32_t)p.dim;
+    const uint32_t b = row / dim;
+    const uint32_t c = row - b * dim;
+    if (t0 + SEG <= (int32_t)p.seqlen) fwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0);
+    else fwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0);
 }
 
 // Channel-last: x[b, c, t] at b*xs0 + c + t*xs2 (unit channel stride).
@@ -220,7 +233,7 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t t = tb + u;
-            xv[u] = (active && t < t1) ? vload(xb + t * xs2) : vzero();
+            xv[u] = (active && t < t1) ? vload_nt(xb + t * xs2) : vzero();
             if constexpr (SEQ) ids[u] = (t < t1) ? sr[t * p.seq_idx_stride[1]] : -1;
         }
 #pragma unroll
@@ -244,7 +257,7 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
                 }
                 o[e] = acc;
             }
-            if (active && t < t1) vstore(ob + t * os2, vpack<T>(o));
+            if (active && t < t1) vstore_nt(ob + t * os2, vpack<T>(o));
 #pragma unroll
             for (int i = 0; i < H; ++i) {
 #pragma unroll
@@ -352,6 +365,9 @@ bool rows_vec_ok(const cc1d_fwd_params& p) {
     if (p.seq_idx != nullptr &&
         (p.seq_idx_stride[1] != 1 || p.seq_idx_stride[0] % 4 != 0 || !aligned16(p.seq_idx)))
         return false;
+    // 32-bit index arithmetic: positions, rows and items (4 per block) must fit
+    if (p.seqlen + 64 * 4 * EPV >= ((int64_t)1 << 31)) return false;
+    if (p.batch * p.dim * ceil_div(p.seqlen, 64 * EPV) * 4 >= ((int64_t)1 << 32)) return false;
     return true;
 }
 
