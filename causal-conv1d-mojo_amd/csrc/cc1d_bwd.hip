@@ -9,14 +9,13 @@
 //   db     += sum_t dpre[t]
 //   dinit[i] = sum_{k<=i} w[k] * dpre[i-k]   (i < W-1)
 // dweight/dbias are reduced in fp32: per lane, across the wavefront
-// (ds_bpermute butterfly), across the block (LDS) and finally one fp32
-// atomic add per (block, tap) into the caller's zeroed accumulator.
+// (ds_bpermute butterfly), then one fp32 atomic add per (wavefront, tap)
+// into the caller's zeroed accumulator -- as in the reference, the order of
+// those adds (over batches and segments) is not fixed.
 //
 // Kernels
-//   bwd_rows_vec -- channel-first rows, same lane layout as fwd_rows_vec.
-//                   All wavefronts of a block work on the same channel (its
-//                   batches / segments), so the weight-gradient partials of a
-//                   channel meet in LDS before touching global memory.
+//   bwd_rows_vec -- channel-first rows, same lane layout and item order as
+//                   fwd_rows_vec (one wavefront per block).
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
 #include "cc1d_internal.hpp"
 
@@ -25,8 +24,7 @@ namespace cc1d {
 struct BwdArgs {
     cc1d_bwd_params p;
     int64_t nseg;     // segments / chunks per row
-    int64_t n_items;  // rows_vec: items per channel (B * nseg); generic: threads
-    int64_t groups;   // rows_vec: blocks per channel
+    int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
     int64_t chunk;    // generic: time steps per thread
 };
 
@@ -35,7 +33,8 @@ struct BwdArgs {
 // whole segment lies inside the row.
 template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
 __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0, const float* w, float bias, float* pw, float& pb) {
+                                                 int32_t t0, const float* w, const float* wq, float bq, float* pw,
+                                                 float& pb) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int SEG = 64 * VPT * EPV;
@@ -131,16 +130,17 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
                 const float g = vget<T>(gv[j], i);
                 float d = g;
                 if constexpr (SILU) {
-                    float pre = bias;
+                    // q = -log2(e) * pre, from pre-scaled weights and bias
+                    float q = bq;
 #pragma unroll
                     for (int k = 0; k < W; ++k) {
                         if constexpr (SEQ) {
-                            if (sw[i + k] == sw[H + i]) pre = __builtin_fmaf(w[k], win[i + k], pre);
+                            if (sw[i + k] == sw[H + i]) q = __builtin_fmaf(wq[k], win[i + k], q);
                         } else {
-                            pre = __builtin_fmaf(w[k], win[i + k], pre);
+                            q = __builtin_fmaf(wq[k], win[i + k], q);
                         }
                     }
-                    d = g * silu_grad(pre);
+                    d = silu_bwd_q(g, q);
                 }
                 if (!FULL && t >= L) d = 0.0f;
                 if constexpr (SEQ) {
@@ -159,9 +159,12 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
             }
         }
 
-        // ---- dpre of the first H positions of the next segment (used by lane 63) ----
+        // ---- dpre of the first H positions of the next segment (used by lane 63;
+        //      zero when this segment ends the row) ----
         float dn[H];
-        {
+#pragma unroll
+        for (int i = 0; i < H; ++i) dn[i] = 0.0f;
+        if (tn < L) {
             float xw[2 * H];
             int32_t iw[2 * H];
 #pragma unroll
@@ -178,16 +181,16 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
                 const float g = vget<T>(gn, i);
                 float d = g;
                 if constexpr (SILU) {
-                    float pre = bias;
+                    float q = bq;
 #pragma unroll
                     for (int k = 0; k < W; ++k) {
                         if constexpr (SEQ) {
-                            if (iw[i + k] == iw[H + i]) pre = __builtin_fmaf(w[k], xw[i + k], pre);
+                            if (iw[i + k] == iw[H + i]) q = __builtin_fmaf(wq[k], xw[i + k], q);
                         } else {
-                            pre = __builtin_fmaf(w[k], xw[i + k], pre);
+                            q = __builtin_fmaf(wq[k], xw[i + k], q);
                         }
                     }
-                    d = g * silu_grad(pre);
+                    d = silu_bwd_q(g, q);
                 }
                 if (tn + i >= L) d = 0.0f;
                 if constexpr (SEQ) {
@@ -260,59 +263,56 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
     }
 }
 
-// Block = one channel c and four (batch, segment) items of it, so the
-// weight-gradient partials of a channel meet in LDS before one fp32 atomic
-// add per tap. All index arithmetic is 32-bit (the launcher checks ranges).
+// One wavefront per block; item = (row, segment) with row = b * dim + c, in
+// memory order like the forward, so consecutive blocks stream consecutive
+// rows. The wavefront reduces its weight/bias-gradient partials with a
+// ds_bpermute butterfly and lanes 0..W add them to the fp32 accumulators
+// (one atomic instruction). All index arithmetic is 32-bit (the launcher
+// checks the ranges).
 template <typename T, int W, int VPT, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(256) bwd_rows_vec(const BwdArgs a) {
+__global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
     constexpr int SEG = 64 * VPT * elems16<T>::value;
     const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const uint32_t groups = (uint32_t)a.groups;
-    const uint32_t c = uniform32(blockIdx.x / groups);
-    const uint32_t it = uniform32((blockIdx.x - c * groups) * 4u + wave);
-    __shared__ float red[4][W + 1];
+    const int lane = threadIdx.x;
+    const uint32_t item = uniform32(blockIdx.x);
+    if (item >= (uint32_t)a.n_items) return;
+    const uint32_t nseg = (uint32_t)a.nseg;
+    const uint32_t row = item / nseg;
+    const int32_t t0 = (int32_t)((item - row * nseg) * SEG);
+    const uint32_t dim = (uint32_t)p.dim;
+    const uint32_t b = row / dim;
+    const uint32_t c = row - b * dim;
 
     float w[W];
     const T* __restrict__ wr = static_cast<const T*>(p.weight) + (int64_t)c * p.weight_stride[0];
 #pragma unroll
     for (int k = 0; k < W; ++k) w[k] = ld(wr, k * p.weight_stride[1]);
     const float bias = p.bias ? ld(static_cast<const T*>(p.bias), (int64_t)c * p.bias_stride) : 0.0f;
+    float wq[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) wq[k] = -kLog2e * w[k];
+    const float bq = -kLog2e * bias;
 
     float pw[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) pw[k] = 0.0f;
     float pb = 0.0f;
+    if (t0 + SEG <= (int32_t)p.seqlen)
+        bwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0, w, wq, bq, pw, pb);
+    else
+        bwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0, w, wq, bq, pw, pb);
 
-    if (it < (uint32_t)a.n_items) {
-        const uint32_t nseg = (uint32_t)a.nseg;
-        const uint32_t b = it / nseg;
-        const int32_t t0 = (int32_t)((it - b * nseg) * SEG);
-        if (t0 + SEG <= (int32_t)p.seqlen)
-            bwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0, w, bias, pw, pb);
-        else
-            bwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0, w, bias, pw, pb);
-    }
-
-    // ---- weight / bias gradient reduction ----
+    // ---- weight / bias gradient: wavefront sum, then lanes 0..W add ----
+    float mine = wave_sum(pb);
 #pragma unroll
-    for (int k = 0; k < W; ++k) pw[k] = wave_sum(pw[k]);
-    pb = wave_sum(pb);
-    if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < W; ++k) red[wave][k] = pw[k];
-        red[wave][W] = pb;
+    for (int k = 0; k < W; ++k) {
+        const float s = wave_sum(pw[k]);
+        if (lane == k) mine = s;
     }
-    __syncthreads();
-    if (threadIdx.x <= W) {
-        const int k = threadIdx.x;
-        const float s = (red[0][k] + red[1][k]) + (red[2][k] + red[3][k]);
-        if (k < W)
-            unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], s);
-        else if (p.dbias_acc != nullptr)
-            unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, s);
-    }
+    if (lane < W)
+        unsafeAtomicAdd(p.dweight_acc + (int64_t)c * p.dweight_acc_stride[0] + lane * p.dweight_acc_stride[1], mine);
+    else if (lane == W && p.dbias_acc != nullptr)
+        unsafeAtomicAdd(p.dbias_acc + (int64_t)c * p.dbias_acc_stride, mine);
 }
 
 template <typename T, int W, bool SILU>
@@ -439,10 +439,9 @@ bool rows_vec_ok(const cc1d_bwd_params& p) {
     if (p.seq_idx != nullptr &&
         (p.seq_idx_stride[1] != 1 || p.seq_idx_stride[0] % 4 != 0 || !aligned16(p.seq_idx)))
         return false;
-    // 32-bit index arithmetic: positions, blocks and items must fit
+    // 32-bit index arithmetic: positions and items (one block each) must fit
     if (p.seqlen + 64 * 4 * EPV >= ((int64_t)1 << 31)) return false;
-    if (p.batch * ceil_div(p.seqlen, 64 * EPV) + 4 >= ((int64_t)1 << 31)) return false;
-    if (p.dim * (p.batch * ceil_div(p.seqlen, 64 * EPV) + 4) >= ((int64_t)1 << 31)) return false;
+    if (p.batch * p.dim * ceil_div(p.seqlen, 64 * EPV) >= ((int64_t)1 << 31)) return false;
     return true;
 }
 
@@ -459,21 +458,19 @@ int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
                 BwdArgs a;
                 a.p = p;
                 a.chunk = 0;
-                a.groups = 0;
                 if constexpr (W - 1 <= EPV) {
                     if (rows_vec_ok<T>(p)) {
                         const int64_t nvec = p.seqlen / EPV;
                         const int64_t per = ceil_div(nvec, 64);
                         const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
-                        a.n_items = p.batch * a.nseg;
-                        a.groups = ceil_div(a.n_items, 4);
-                        const dim3 grid((unsigned)(p.dim * a.groups));
+                        a.n_items = p.batch * p.dim * a.nseg;
+                        const dim3 grid((unsigned)a.n_items);
                         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                             constexpr bool SEQ = decltype(qc)::value;
-                            if (vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                            else if (vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                            else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                            if (vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                            else if (vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                            else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
                             return launch_status();
                         });
                     }

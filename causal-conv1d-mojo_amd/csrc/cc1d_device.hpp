@@ -103,6 +103,18 @@ __device__ __forceinline__ float silu_grad(float x) {
     return s * (1.0f + x * (1.0f - s));
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// g * silu'(p) given q = -log2(e) * p (so exp(-p) = exp2(q)):
+//   s = 1 / (1 + exp2(q));  g * s * (1 + p * (1 - s)) = gs + (gs * q) * (-ln2 * (1 - s))
+// Five VALU operations plus exp2 and rcp.
+__device__ __forceinline__ float silu_bwd_q(float g, float q) {
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(q));
+    const float gs = g * s;
+    return __builtin_fmaf(gs * q, __builtin_fmaf(s, kLn2, -kLn2), gs);
+}
+
 // Causal taps: bias + sum_k w[k] * win[k], fp32 fma in k order. The forward
 // and the decode update both use this, so a decode loop reproduces the full
 // forward bit for bit.

@@ -194,13 +194,26 @@ def test_zero_sized_backward(shape, has_init):
         assert torch.all(init.grad == 0)
 
 
-def test_backward_repeat_is_deterministic_for_one_block_per_channel():
-    """B * segments <= 4: each channel's weight gradient has a single writer."""
-    x, w, b, _ = make_inputs(4, 128, 2048, 4, dtype=torch.bfloat16)
-    dout = make_inputs(4, 128, 2048, 4, dtype=torch.bfloat16, seed=1)[0]
+def test_backward_repeat_single_contribution_is_bit_identical():
+    """One (batch, segment) per channel: each weight-gradient entry receives a
+    single fp32 add, so repeated backward passes agree bit for bit."""
+    x, w, b, _ = make_inputs(1, 128, 2048, 4, dtype=torch.bfloat16)
+    dout = make_inputs(1, 128, 2048, 4, dtype=torch.bfloat16, seed=1)[0]
     a = _gpu_grads(x, w, b, dout, activation="silu")
     for _ in range(2):
         again = _gpu_grads(x, w, b, dout, activation="silu")
         for u, v in zip(a, again):
             if u is not None:
                 assert torch.equal(u, v)
+
+
+def test_backward_repeat_multi_batch_within_tolerance():
+    """Several batches per channel: the fp32 atomic adds land in any order (as in
+    the reference), so repeats agree to fp32 rounding; dx is still bit-identical."""
+    x, w, b, _ = make_inputs(4, 128, 2048, 4, dtype=torch.float32)
+    dout = make_inputs(4, 128, 2048, 4, dtype=torch.float32, seed=1)[0]
+    a = _gpu_grads(x, w, b, dout, activation="silu")
+    again = _gpu_grads(x, w, b, dout, activation="silu")
+    assert torch.equal(a[0], again[0])
+    assert_reduction_close(a[1], again[1], torch.float32)
+    assert_reduction_close(a[2], again[2], torch.float32)

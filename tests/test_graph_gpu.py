@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import causal_conv1d_amd as cc
-from _util import make_inputs
+from _util import assert_reduction_close, make_inputs
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -68,8 +68,12 @@ def test_backward_ops_capture_replay_matches_eager():
         snap = [t.clone() for t in (out, dx, dw, db)]
         step()
         torch.cuda.synchronize()
-        for name, a, e in zip(("out", "dx", "dweight", "dbias"), snap, (out, dx, dw, db)):
+        for name, a, e in zip(("out", "dx"), snap[:2], (out, dx)):
             assert torch.equal(a, e), f"replay {i}: {name}"
+        # dweight / dbias gather B fp32 atomic adds per entry in any order: equal up
+        # to fp32 rounding (a missing zero-fill on replay would double them)
+        for name, a, e in zip(("dweight", "dbias"), snap[2:], (dw, db)):
+            assert_reduction_close(a, e, torch.float32, name=f"replay {i}: {name}")
 
 
 def test_update_capture_replay_matches_eager():
