@@ -65,6 +65,7 @@ def _parse():
     ap.add_argument("--mode", choices=["bench", "kernels", "copy"], default="bench")
     ap.add_argument("--launches", type=int, default=40, help="launches per kernel timing graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C3/C4b/C5 report lines")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
     return ap.parse_args()
 
@@ -219,6 +220,96 @@ def bench_update(torch, cc, launches):
     return res
 
 
+def _time_launch_set(torch, fns, launches):
+    """Average ms per launch of a graph that cycles through the closures `fns`."""
+    def loop():
+        for i in range(launches):
+            fns[i % len(fns)]()
+    g = _graph(torch, loop)
+    ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
+    del g
+    return ms
+
+
+def _entry(ms, nbytes, **extra):
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1),
+            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), **extra}
+
+
+def bench_configs(torch, cc, launches):
+    """Kernel throughput at the other BASELINE configurations (reported, not the headline)."""
+    ops = torch.ops.causal_conv1d_amd
+    res = {}
+    # C3: stored (1, 8192, 4096) bf16 channel-last, viewed (1, 4096, 8192); W4, SiLU, no bias
+    L3, D3 = 8192, 4096
+    sets = []
+    g = torch.Generator(device="cuda").manual_seed(3)
+    w3 = torch.randn(D3, W, generator=g, device="cuda").bfloat16()
+    cuts = torch.sort(torch.randperm(L3 - 1, generator=torch.Generator().manual_seed(0))[:7] + 1).values
+    seq = torch.zeros(1, L3, dtype=torch.int32)
+    for i, c in enumerate(cuts.tolist()):
+        seq[:, c:] = i + 1
+    seq = seq.cuda()
+    init = torch.randn(1, D3, W - 1, generator=g, device="cuda").bfloat16()
+    for _ in range(3):
+        x = torch.randn(1, L3, D3, generator=g, device="cuda").bfloat16().transpose(1, 2)
+        dout = torch.randn(1, L3, D3, generator=g, device="cuda").bfloat16().transpose(1, 2)
+        sets.append((x, dout, torch.empty_like(x), torch.empty_like(x)))
+    dw3 = torch.zeros(D3, W, dtype=torch.float32, device="cuda")
+    fs = torch.empty(1, D3, W - 1, dtype=torch.bfloat16, device="cuda")
+    di = torch.empty_like(init)
+    n3 = L3 * D3 * 2
+    for name, kw_f, kw_b, extra_f, extra_b in (
+            ("c3a", (seq, None, None), (seq, None), 32768 + D3 * W * 2, 2 * 32768 + D3 * W * 2 + D3 * W * 4),
+            ("c3b", (None, init, fs), (None, init), D3 * W * 2 + 2 * 24576, D3 * W * 2 + D3 * W * 4 + 2 * 24576)):
+        s_, i_, f_ = kw_f
+        fns = [lambda x=x, o=o: ops._fwd_inplace(x, w3, None, s_, i_, o, True, f_) for x, _, o, _ in sets]
+        res[f"{name}_fwd"] = _entry(_time_launch_set(torch, fns, launches), 2 * n3 + extra_f)
+        sb, ib = kw_b
+        fns = [lambda x=x, d=d, dx=dx: ops._bwd_full_inplace(x, w3, None, d, sb, ib, dx, dw3, None,
+                                                             di if ib is not None else None, True)
+               for x, d, _, dx in sets]
+        res[f"{name}_bwd"] = _entry(_time_launch_set(torch, fns, launches), 3 * n3 + extra_b)
+        log(f"{name}: fwd {res[name + '_fwd']['us_per_launch']} us, bwd {res[name + '_bwd']['us_per_launch']} us")
+    del sets
+    # C5: (8, 2048, 16384), no bias, no activation, bf16 and fp32 at W4 (W2/W3 in the tests)
+    B5, D5, L5 = 8, 2048, 16384
+    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
+        es = 2 if dt == torch.bfloat16 else 4
+        x = torch.randn(B5, D5, L5, generator=g, device="cuda").to(dt)
+        dout = torch.randn(B5, D5, L5, generator=g, device="cuda").to(dt)
+        out, dx = torch.empty_like(x), torch.empty_like(x)
+        w5 = torch.randn(D5, W, generator=g, device="cuda").to(dt)
+        dw5 = torch.zeros(D5, W, dtype=torch.float32, device="cuda")
+        n5 = B5 * D5 * L5 * es
+        nl = max(4, launches // 8)
+        res[f"c5_{tag}_fwd"] = _entry(_time_launch_set(
+            torch, [lambda: ops._fwd_inplace(x, w5, None, None, None, out, False, None)], nl), 2 * n5 + D5 * W * es)
+        res[f"c5_{tag}_bwd"] = _entry(_time_launch_set(
+            torch, [lambda: ops._bwd_full_inplace(x, w5, None, dout, None, None, dx, dw5, None, None, False)], nl),
+            3 * n5 + D5 * W * (es + 4))
+        log(f"c5 {tag}: fwd {res[f'c5_{tag}_fwd']['us_per_launch']} us, bwd {res[f'c5_{tag}_bwd']['us_per_launch']} us")
+        del x, dout, out, dx
+    # C4b: x (256, 5120, 4), circular state_len 64 in a pool of 512, cache_seqlens in [0, 64)
+    usets = []
+    w4 = torch.randn(D, W, generator=g, device="cuda").bfloat16()
+    b4 = torch.randn(D, generator=g, device="cuda").bfloat16()
+    for _ in range(4):
+        x = torch.randn(UPD_B, D, 4, generator=g, device="cuda").bfloat16()
+        pool = torch.randn(UPD_POOL, D, 64, generator=g, device="cuda").bfloat16()
+        idx = torch.randperm(UPD_POOL, generator=g, device="cuda")[:UPD_B].to(torch.int32)
+        cs = torch.randint(0, 64, (UPD_B,), generator=g, device="cuda", dtype=torch.int32)
+        usets.append((x, pool, idx, cs, torch.empty_like(x)))
+    fns = [lambda u=u: cc._native.native_update(u[0], w4, b4, u[1], u[2], u[3], u[4], True) for u in usets]
+    ms = _time_launch_set(torch, fns, launches)
+    nb = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4
+    res["update_c4b"] = _entry(ms, nb, us_per_call=round(ms * 1e3, 2),
+                               note="14 of 128 bytes of each state row are touched; DRAM bursts bound this")
+    log(f"c4b update: {res['update_c4b']['us_per_launch']} us")
+    return res
+
+
 def cpu_baseline(torch, seconds):
     """The CPU oracle on a bounded sample of C2 (512 of the 5120 channels, all 4
     batches, full length), fwd + bwd repeated for about `seconds`."""
@@ -316,6 +407,9 @@ def main():
     del sets
     torch.cuda.empty_cache()
     upd = bench_update(torch, cc, args.launches)
+    torch.cuda.empty_cache()
+    cfgs = {} if args.no_configs else bench_configs(torch, cc, args.launches)
+    torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, args.cpu_seconds)
 
     step_bytes = FWD_BYTES + BWD_BYTES
@@ -351,7 +445,7 @@ def main():
             "algorithmic_bytes_per_launch": BWD_BYTES,
             "us_per_launch": bwd["us_per_launch"],
         },
-        "kernels": {"fwd": kern["fwd"], "bwd": kern["bwd"], "update_c4a": upd},
+        "kernels": {"fwd": kern["fwd"], "bwd": kern["bwd"], "update_c4a": upd, **cfgs},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -13,8 +13,10 @@
 // Kernels
 //   update_vec1    -- linear mode, one token, S == W-1, channel-contiguous x /
 //                     out and contiguous state rows: a lane owns EPV adjacent
-//                     channels, so x, out, weight and the (EPV x S) state
-//                     block move as 16-byte vectors.
+//                     channels of 2 batch entries, so x, out, weight and the
+//                     (EPV x S) state blocks move as 16-byte vectors.
+//   update_circ    -- circular mode with up to 8 new tokens; one thread per
+//                     (b, c) with all loads issued before any store.
 //   update_generic -- everything else; one thread per (b, c).
 // Both use the forward's tap loop (fma in k order, then SiLU), so a decode
 // loop reproduces the full forward bit for bit.
@@ -100,62 +102,150 @@ __global__ void __launch_bounds__(256) update_generic(const UpdArgs a) {
     }
 }
 
-// Linear mode, seqlen 1, state_len == W-1. Lane -> (b, EPV channels).
-template <typename T, int W, bool SILU>
+// Linear mode, seqlen 1, state_len == W-1. A lane owns EPV adjacent channels
+// of BPL consecutive batch entries: the weight/bias vectors are loaded once
+// for the BPL entries, and all loads are issued unconditionally (entries
+// past the batch or padding entries read row 0 / entry 0) before the
+// arithmetic; only the stores are predicated. Lanes run along channels, so
+// x, out and the (EPV x S) state blocks of one entry are contiguous spans.
+template <typename T, int W, bool SILU, int BPL>
 __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int NV = H;  // 16-byte vectors in an (EPV x H) state block
     const cc1d_update_params& p = a.p;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.n_items) return;
-    const int64_t g = idx % a.ngroups;
-    const int64_t b = idx / a.ngroups;
-    const int64_t c0 = g * EPV;
-    T* __restrict__ op = static_cast<T*>(p.out) + b * p.out_stride[0] + c0;
-    const int64_t row = state_row(p, b);
-    if (row < 0) {
-        vstore(op, vzero());
-        return;
-    }
-    const u32x4 xv = vload(static_cast<const T*>(p.x) + b * p.x_stride[0] + c0);
-    T* __restrict__ sp = static_cast<T*>(p.conv_state) + row * p.conv_state_stride[0] + c0 * H;
-    u32x4 sv[NV];
-#pragma unroll
-    for (int n = 0; n < NV; ++n) sv[n] = vload(sp + n * EPV);
-    // contiguous (dim, W) weight: EPV*W values = W vectors
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= (uint32_t)a.n_items) return;
+    const uint32_t ng = (uint32_t)a.ngroups;
+    const uint32_t b0 = (idx / ng) * BPL;
+    const uint32_t c0 = (idx - (idx / ng) * ng) * EPV;
+    const uint32_t nb = (uint32_t)p.batch;
+
+    const T* wp = static_cast<const T*>(p.weight) + (size_t)c0 * W;
     u32x4 wv[W];
-    const T* wp = static_cast<const T*>(p.weight) + c0 * W;
 #pragma unroll
     for (int n = 0; n < W; ++n) wv[n] = vload(wp + n * EPV);
-    u32x4 bv = vzero();
-    if (p.bias) bv = vload(static_cast<const T*>(p.bias) + c0);
+    const u32x4 bv = p.bias ? vload(static_cast<const T*>(p.bias) + c0) : vzero();
 
-    float o[EPV];
-    float ns[EPV * H];
+    int32_t row[BPL];
+    u32x4 xv[BPL], sv[BPL][NV];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-        float win[W], w[W];
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-            const int n = e * H + i;
-            win[i] = vget<T>(sv[n / EPV], n % EPV);
+    for (int q = 0; q < BPL; ++q) {
+        const uint32_t b = b0 + q < nb ? b0 + q : 0;
+        int32_t r = (int32_t)b;
+        if (p.conv_state_indices != nullptr) {
+            r = p.conv_state_indices[b];
+            if (r >= p.state_rows) r = -1;
         }
-        win[H] = vget<T>(xv, e);
+        row[q] = (b0 + q < nb) ? r : -2;
+        const uint32_t rr = r >= 0 ? (uint32_t)r : 0u;
+        xv[q] = vload(static_cast<const T*>(p.x) + (size_t)b * p.x_stride[0] + c0);
+        const T* sp = static_cast<const T*>(p.conv_state) + (size_t)rr * p.conv_state_stride[0] + (size_t)c0 * H;
 #pragma unroll
-        for (int k = 0; k < W; ++k) {
-            const int n = e * W + k;
-            w[k] = vget<T>(wv[n / EPV], n % EPV);
-        }
-        float acc = conv_taps<W>(vget<T>(bv, e), w, win);
-        if constexpr (SILU) acc = silu(acc);
-        o[e] = acc;
-#pragma unroll
-        for (int i = 0; i < H; ++i) ns[e * H + i] = win[i + 1];
+        for (int n = 0; n < NV; ++n) sv[q][n] = vload(sp + n * EPV);
     }
-    vstore(op, vpack<T>(o));
 #pragma unroll
-    for (int n = 0; n < NV; ++n) vstore(sp + n * EPV, vpack<T>(ns + n * EPV));
+    for (int q = 0; q < BPL; ++q) {
+        float o[EPV];
+        float ns[EPV * H];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            float win[W], w[W];
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const int n = e * H + i;
+                win[i] = vget<T>(sv[q][n / EPV], n % EPV);
+            }
+            win[H] = vget<T>(xv[q], e);
+#pragma unroll
+            for (int k = 0; k < W; ++k) {
+                const int n = e * W + k;
+                w[k] = vget<T>(wv[n / EPV], n % EPV);
+            }
+            float acc = conv_taps<W>(vget<T>(bv, e), w, win);
+            if constexpr (SILU) acc = silu(acc);
+            o[e] = acc;
+#pragma unroll
+            for (int i = 0; i < H; ++i) ns[e * H + i] = win[i + 1];
+        }
+        if (row[q] == -2) continue;  // past the batch
+        T* op = static_cast<T*>(p.out) + (size_t)(b0 + q) * p.out_stride[0] + c0;
+        if (row[q] < 0) {  // padding (or out-of-pool) entry: zero output, state untouched
+            vstore(op, vzero());
+            continue;
+        }
+        vstore(op, vpack<T>(o));
+        T* sp = static_cast<T*>(p.conv_state) + (size_t)row[q] * p.conv_state_stride[0] + (size_t)c0 * H;
+#pragma unroll
+        for (int n = 0; n < NV; ++n) vstore(sp + n * EPV, vpack<T>(ns + n * EPV));
+    }
+}
+
+// Circular mode with at most LMAX new tokens: one thread per (b, c), lanes on
+// adjacent channels. Every load (W-1 history values, the new tokens) is
+// issued before any arithmetic or store, so each lane keeps all of its
+// scattered state accesses in flight at once.
+template <typename T, int W, bool SILU, int LMAX>
+__global__ void __launch_bounds__(256) update_circ(const UpdArgs a) {
+    constexpr int H = W - 1;
+    const cc1d_update_params& p = a.p;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n_items) return;
+    const int64_t c = idx % p.dim;
+    const int64_t b = idx / p.dim;
+    const int Ls = (int)p.seqlen;
+    const int64_t S = p.state_len;
+    T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+    const int64_t row = state_row(p, b);
+    if (row < 0) {
+#pragma unroll
+        for (int i = 0; i < LMAX; ++i)
+            if (i < Ls) st(orow, i * p.out_stride[2], 0.0f);
+        return;
+    }
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+    T* __restrict__ sr = static_cast<T*>(p.conv_state) + row * p.conv_state_stride[0] + c * p.conv_state_stride[1];
+    const int64_t ss = p.conv_state_stride[2];
+    int64_t cs = (int64_t)p.cache_seqlens[b] % S;
+    if (cs < 0) cs += S;  // floored modulo (torch.remainder)
+    int64_t head = cs - H;
+    if (head < 0) head += S;
+
+    T hist[H > 0 ? H : 1];
+    T xv[LMAX];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        int64_t pos = head + i;
+        if (pos >= S) pos -= S;
+        hist[i] = sr[pos * ss];
+    }
+#pragma unroll
+    for (int i = 0; i < LMAX; ++i)
+        if (i < Ls) xv[i] = xr[i * p.x_stride[2]];
+
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        w[k] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
+
+    float win[W];
+#pragma unroll
+    for (int i = 0; i < H; ++i) win[i] = to_f32(hist[i]);
+    int64_t wpos = cs;
+#pragma unroll
+    for (int i = 0; i < LMAX; ++i) {
+        if (i < Ls) {
+            sr[wpos * ss] = xv[i];
+            if (++wpos >= S) wpos -= S;
+            win[H] = to_f32(xv[i]);
+            float acc = conv_taps<W>(bias, w, win);
+            if constexpr (SILU) acc = silu(acc);
+            st(orow, i * p.out_stride[2], acc);
+#pragma unroll
+            for (int k = 0; k < H; ++k) win[k] = win[k + 1];
+        }
+    }
 }
 
 namespace {
@@ -172,6 +262,8 @@ bool vec1_ok(const cc1d_update_params& p) {
     if (p.weight_stride[1] != 1 || p.weight_stride[0] != p.width) return false;
     if (p.bias != nullptr && (p.bias_stride != 1 || !aligned16(p.bias))) return false;
     if (!aligned16(p.x) || !aligned16(p.out) || !aligned16(p.conv_state) || !aligned16(p.weight)) return false;
+    // 32-bit lane indices; size_t offsets
+    if (p.batch * p.dim >= ((int64_t)1 << 31) || p.state_rows >= ((int64_t)1 << 31)) return false;
     return true;
 }
 
@@ -189,13 +281,18 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                 a.p = p;
                 a.ngroups = 0;
                 if (vec1_ok<T>(p)) {
+                    constexpr int BPL = 2;
                     a.ngroups = p.dim / EPV;
-                    a.n_items = p.batch * a.ngroups;
-                    update_vec1<T, W, SILU><<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
+                    a.n_items = ceil_div(p.batch, BPL) * a.ngroups;
+                    update_vec1<T, W, SILU, BPL><<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
                     return launch_status();
                 }
                 a.n_items = p.batch * p.dim;
                 const dim3 grid((unsigned)ceil_div(a.n_items, 256));
+                if (p.cache_seqlens != nullptr && p.seqlen <= 8) {
+                    update_circ<T, W, SILU, 8><<<grid, 256, 0, stream>>>(a);
+                    return launch_status();
+                }
                 return with_flag(p.cache_seqlens != nullptr, [&](auto cc) {
                     constexpr bool CIRC = decltype(cc)::value;
                     update_generic<T, W, SILU, CIRC><<<grid, 256, 0, stream>>>(a);
