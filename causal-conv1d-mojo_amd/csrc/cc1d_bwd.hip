@@ -16,6 +16,8 @@
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
 //                   fwd_rows_vec (one wavefront per block).
+//   bwd_cols_vec -- channel-last (unit channel stride); lanes own adjacent
+//                   channels and walk a tile of time steps.
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
 #include "cc1d_internal.hpp"
 
@@ -23,10 +25,16 @@ namespace cc1d {
 
 struct BwdArgs {
     cc1d_bwd_params p;
-    int64_t nseg;     // segments / chunks per row
-    int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
-    int64_t chunk;    // generic: time steps per thread
+    int64_t nseg;     // segments / tiles / chunks per row
+    int64_t n_items;  // rows_vec: (row, segment) items; cols: wavefronts; generic: threads
+    int64_t chunk;    // cols / generic: time steps per item
+    int64_t groups;   // cols: channel groups of 64 * CPL
 };
+
+// channel-last launch shape: channels per lane, steps per tile, steps in flight
+constexpr int kBwdColsCPL = 2;
+constexpr int64_t kBwdColsChunk = 64;
+constexpr int kBwdColsU = 4;
 
 // One wavefront-segment of row (b, c): writes dx (and dinitial_states) and
 // adds this segment's weight/bias-gradient partials into pw / pb. FULL: the
@@ -315,6 +323,230 @@ __global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
         unsafeAtomicAdd(p.dbias_acc + (int64_t)c * p.dbias_acc_stride, mine);
 }
 
+// Wavefront-scope barrier for an LDS exchange between the lanes of one
+// wavefront (orders this wavefront's LDS writes before its reads).
+__device__ __forceinline__ void wave_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Channel-last backward: x / dout / dx have unit channel stride. Work item =
+// (b, tile of `chunk` steps, group of 64*CPL channels), group fastest; a
+// lane owns CPL adjacent channels. The wavefront walks s = t0 .. t1+W-2:
+// dpre[s] needs x[s-W+1 .. s] (register window) and dout[s]; once dpre[s] is
+// known, dx[s-W+1] is complete. The W-1 steps past the tile are recomputed
+// (they are the next tile's first steps). Loads are double-buffered: the
+// next U steps are in flight while the current U are computed. seq_idx is
+// one value per step, identical for every lane. At the end the lanes'
+// weight/bias-gradient partials are transposed through LDS so that the fp32
+// atomic adds of a wavefront land on consecutive addresses.
+template <typename T, int W, int CPL, int U, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(256) bwd_cols_vec(const BwdArgs a) {
+    constexpr int H = W - 1;
+    constexpr int NR = 64 * CPL;  // channels per wavefront
+    static_assert(U >= H, "the first step group must cover the W-1 initial positions");
+    using V = Lanes<T, CPL>;
+    __shared__ float red[4][NR * (W + 1)];
+    const cc1d_bwd_params& p = a.p;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t item = uniform((int64_t)blockIdx.x * 4 + wave);
+    if (item >= a.n_items) return;
+    const int64_t g = item % a.groups;
+    const int64_t rest = item / a.groups;
+    const int64_t tile = rest % a.nseg;
+    const int64_t b = rest / a.nseg;
+    const int64_t cw0 = g * NR;  // first channel of this wavefront
+    const int64_t c0 = cw0 + lane * CPL;
+    const bool active = c0 < p.dim;
+    const int64_t L = p.seqlen;
+    const int64_t t0 = tile * a.chunk;
+    const int64_t t1 = (t0 + a.chunk < L) ? t0 + a.chunk : L;
+    const int64_t send = (t1 + H < L) ? t1 + H : L;  // positions whose dpre is needed
+    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
+    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
+    T* __restrict__ db = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
+    const int64_t xs2 = p.x_stride[2], gs2 = p.dout_stride[2], ds2 = p.dx_stride[2];
+    const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
+
+    float w[W][CPL], wq[W][CPL], bq[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        const int64_t c = active ? c0 + e : 0;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+            wq[k][e] = -kLog2e * w[k][e];
+        }
+        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
+    }
+
+    // windows over positions s-H .. s
+    float xw[W][CPL], dw[W][CPL];
+    int32_t iw[W];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        const int64_t s = t0 - H + i;
+        V hv;
+        hv.zero();
+        if (active && s >= 0) hv.template load<false>(xb + s * xs2);
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            xw[i][e] = hv.get(e);
+            dw[i][e] = 0.0f;
+        }
+        if (s < 0 && p.initial_states != nullptr && active) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e)
+                xw[i][e] = ld(static_cast<const T*>(p.initial_states),
+                              b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
+                                  (s + H) * p.initial_states_stride[2]);
+        }
+        iw[i] = (SEQ && s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
+    }
+    float pw[W][CPL], pb[CPL], dfirst[H > 0 ? H : 1][CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        pb[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) pw[k][e] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < H; ++i) dfirst[i][e] = 0.0f;
+    }
+    const int64_t m = (H < L) ? H : L;  // dfinal tail length
+
+    auto load_group = [&](V* xv, V* gv, int32_t* ids, int64_t sb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t s = sb + u;
+            xv[u].zero();
+            gv[u].zero();
+            if (active && s < send) {
+                xv[u].template load<true>(xb + s * xs2);
+                gv[u].template load<true>(gb + s * gs2);
+            }
+            ids[u] = (SEQ && s < send) ? sr[s * p.seq_idx_stride[1]] : -1;
+        }
+    };
+    auto run_group = [&](const V* xv, const V* gv, const int32_t* ids, int64_t sb) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t s = sb + u;
+            if (s >= t1 + H) break;
+            const bool in = s < L;
+            iw[H] = ids[u];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                xw[H][e] = xv[u].get(e);
+                const float gval = gv[u].get(e);
+                float d = gval;
+                if constexpr (SILU) {
+                    float q = bq[e];
+#pragma unroll
+                    for (int k = 0; k < W; ++k) {
+                        if (!SEQ || iw[k] == iw[H]) q = __builtin_fmaf(wq[k][e], xw[k][e], q);
+                    }
+                    d = silu_bwd_q(gval, q);
+                }
+                if (!in || (SEQ && iw[H] < 0)) d = 0.0f;
+                dw[H][e] = d;
+                if (s < t1) {
+                    pb[e] += d;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) {
+                        if (!SEQ || iw[k] == iw[H]) pw[k][e] = __builtin_fmaf(d, xw[k][e], pw[k][e]);
+                    }
+                }
+            }
+            if (sb == 0 && u < H) {  // dpre[0 .. W-2] for dinitial_states (t0 == 0)
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) dfirst[u < H ? u : 0][e] = dw[H][e];
+            }
+            const int64_t q = s - H;  // dx[q] is complete
+            if (q >= t0) {
+                float o[CPL];
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) {
+                        if (!SEQ || iw[k] == iw[0]) acc = __builtin_fmaf(w[H - k][e], dw[k][e], acc);
+                    }
+                    if (p.dfinal_states != nullptr && q >= L - m && active)
+                        acc = round_to<T>(acc) + ld(static_cast<const T*>(p.dfinal_states),
+                                                    b * p.dfinal_states_stride[0] + (c0 + e) * p.dfinal_states_stride[1] +
+                                                        (q - L + H) * p.dfinal_states_stride[2]);
+                    o[e] = acc;
+                }
+                if (active) {
+                    V ov;
+                    ov.set(o);
+                    ov.template store<true>(db + q * ds2);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) {
+                    xw[i][e] = xw[i + 1][e];
+                    dw[i][e] = dw[i + 1][e];
+                }
+                iw[i] = iw[i + 1];
+            }
+        }
+    };
+    V xa[U], ga[U], xc[U], gc[U];
+    int32_t ia[U], ic[U];
+    load_group(xa, ga, ia, t0);
+    for (int64_t sb = t0; sb < t1 + H; sb += 2 * U) {
+        load_group(xc, gc, ic, sb + U);
+        run_group(xa, ga, ia, sb);
+        load_group(xa, ga, ia, sb + 2 * U);
+        if (sb + U < t1 + H) run_group(xc, gc, ic, sb + U);
+    }
+
+    if (p.dinitial_states != nullptr && t0 == 0 && active) {
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
+                    (c0 + e) * p.dinitial_states_stride[1];
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], dfirst[i - k][e], acc);
+                st(di, i * p.dinitial_states_stride[2], acc);
+            }
+        }
+    }
+
+    // ---- weight / bias gradient: transpose through LDS, then consecutive atomics ----
+    float* r = red[wave];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+#pragma unroll
+        for (int k = 0; k < W; ++k) r[(lane * CPL + e) * W + k] = pw[k][e];
+        r[NR * W + lane * CPL + e] = pb[e];
+    }
+    wave_lds_barrier();
+#pragma unroll
+    for (int j = 0; j < CPL * W; ++j) {
+        const int idx = j * 64 + lane;  // (channel, tap) pair, taps fastest
+        const int64_t c = cw0 + idx / W;
+        if (c < p.dim)
+            unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + (idx % W) * p.dweight_acc_stride[1], r[idx]);
+    }
+    if (p.dbias_acc != nullptr) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int idx = j * 64 + lane;
+            const int64_t c = cw0 + idx;
+            if (c < p.dim) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, r[NR * W + idx]);
+        }
+    }
+}
+
 template <typename T, int W, bool SILU>
 __global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
     constexpr int H = W - 1;
@@ -445,6 +677,20 @@ bool rows_vec_ok(const cc1d_bwd_params& p) {
     return true;
 }
 
+template <typename T, int CPL>
+bool cols_vec_ok(const cc1d_bwd_params& p) {
+    constexpr int64_t NB = CPL * (int64_t)sizeof(T);
+    if (p.x_stride[1] != 1 || p.dout_stride[1] != 1 || p.dx_stride[1] != 1) return false;
+    if (p.dim % CPL != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.dout) |
+         reinterpret_cast<uintptr_t>(p.dx)) % NB)
+        return false;
+    if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.dout_stride[0] % CPL || p.dout_stride[2] % CPL ||
+        p.dx_stride[0] % CPL || p.dx_stride[2] % CPL)
+        return false;
+    return true;
+}
+
 }  // namespace
 
 int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
@@ -458,6 +704,7 @@ int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
                 BwdArgs a;
                 a.p = p;
                 a.chunk = 0;
+                a.groups = 0;
                 if constexpr (W - 1 <= EPV) {
                     if (rows_vec_ok<T>(p)) {
                         const int64_t nvec = p.seqlen / EPV;
@@ -474,6 +721,20 @@ int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
                             return launch_status();
                         });
                     }
+                }
+                constexpr int CPL = kBwdColsCPL;
+                if (cols_vec_ok<T, CPL>(p)) {
+                    a.groups = ceil_div(p.dim / CPL, 64);
+                    a.chunk = kBwdColsChunk;
+                    a.nseg = ceil_div(p.seqlen, a.chunk);
+                    a.n_items = p.batch * a.nseg * a.groups;
+                    const dim3 grid((unsigned)ceil_div(a.n_items, 4));
+                    return with_flag(p.seq_idx != nullptr, [&](auto qc) {
+                        constexpr bool SEQ = decltype(qc)::value;
+                        bwd_cols_vec<T, W, CPL, (kBwdColsU > W - 1 ? kBwdColsU : W - 1), SILU, SEQ>
+                            <<<grid, 256, 0, stream>>>(a);
+                        return launch_status();
+                    });
                 }
                 a.chunk = 64;
                 a.nseg = ceil_div(p.seqlen, a.chunk);

@@ -89,6 +89,73 @@ template <typename T> __device__ __forceinline__ void vstore_nt(T* p, const u32x
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// N consecutive elements of T held as raw dwords, N * sizeof(T) in {4, 8, 16}
+// (one global_load / store of 1, 2 or 4 dwords per lane). Element indices
+// are compile-time after unrolling.
+template <typename T, int N> struct Lanes {
+    static constexpr int ND = N * (int)sizeof(T) / 4;
+    static_assert(ND == 1 || ND == 2 || ND == 4, "4, 8 or 16 bytes per lane");
+    uint32_t d[ND];
+
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < ND; ++i) d[i] = 0u;
+    }
+    template <bool NT> __device__ __forceinline__ void load(const T* p) {
+        if constexpr (ND == 4) {
+            const u32x4 v = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p))
+                               : *reinterpret_cast<const u32x4*>(p);
+            d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+        } else if constexpr (ND == 2) {
+            const u32x2 v = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p))
+                               : *reinterpret_cast<const u32x2*>(p);
+            d[0] = v[0]; d[1] = v[1];
+        } else {
+            d[0] = NT ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p))
+                      : *reinterpret_cast<const uint32_t*>(p);
+        }
+    }
+    template <bool NT> __device__ __forceinline__ void store(T* p) const {
+        if constexpr (ND == 4) {
+            const u32x4 v = {d[0], d[1], d[2], d[3]};
+            if (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+            else *reinterpret_cast<u32x4*>(p) = v;
+        } else if constexpr (ND == 2) {
+            const u32x2 v = {d[0], d[1]};
+            if (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+            else *reinterpret_cast<u32x2*>(p) = v;
+        } else {
+            if (NT) __builtin_nontemporal_store(d[0], reinterpret_cast<uint32_t*>(p));
+            else *reinterpret_cast<uint32_t*>(p) = d[0];
+        }
+    }
+    __device__ __forceinline__ float get(int e) const {
+        if constexpr (sizeof(T) == 4) {
+            return __uint_as_float(d[e]);
+        } else {
+            const uint32_t w = d[e >> 1];
+            if constexpr (__is_same(T, bf16)) {
+                return (e & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+            } else {
+                const uint16_t h = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+                return (float)__builtin_bit_cast(_Float16, h);
+            }
+        }
+    }
+    __device__ __forceinline__ void set(const float* f) {
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int i = 0; i < ND; ++i) d[i] = __float_as_uint(f[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < ND; ++i)
+                d[i] = (uint32_t)from_f32<T>(f[2 * i]).bits | ((uint32_t)from_f32<T>(f[2 * i + 1]).bits << 16);
+        }
+    }
+};
+
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
 template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 

@@ -168,25 +168,24 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
 }
 
 // Channel-last: x[b, c, t] at b*xs0 + c + t*xs2 (unit channel stride).
-// Work item = (b, channel group of 64*EPV channels, tile of `chunk` steps);
-// each wavefront walks its tile with all loads of an unrolled group issued
-// before the arithmetic.
-template <typename T, int W, bool SILU, bool SEQ>
+// Work item = (b, tile of `chunk` steps, group of 64*CPL channels), group
+// fastest. A lane owns CPL adjacent channels (one CPL-element vector per
+// time step) and walks its tile with a register window of the previous W-1
+// steps; the U loads of a step group are issued before their arithmetic.
+// seq_idx is one value per time step here, identical for every lane.
+template <typename T, int W, int CPL, int U, bool SILU, bool SEQ>
 __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
-    constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
-    constexpr int U = 8;  // time steps in flight per lane
+    using V = Lanes<T, CPL>;
     const cc1d_fwd_params& p = a.p;
     const int lane = threadIdx.x & 63;
     const int64_t item = uniform((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6));
     if (item >= a.n_items) return;
-    // item -> (b, tile, group) with the channel group fastest so that the
-    // wavefronts of one block read adjacent channels of the same time steps.
     const int64_t g = item % a.ngroups;
     const int64_t rest = item / a.ngroups;
     const int64_t tile = rest % a.nseg;
     const int64_t b = rest / a.nseg;
-    const int64_t c0 = (g * 64 + lane) * EPV;
+    const int64_t c0 = (g * 64 + lane) * CPL;
     const bool active = c0 < p.dim;
     const int64_t L = p.seqlen;
     const int64_t t0 = tile * a.chunk;
@@ -195,10 +194,10 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
     const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
     T* __restrict__ ob = static_cast<T*>(p.out) + b * p.out_stride[0] + c0;
 
-    float w[W][EPV];
-    float bias[EPV];
+    float w[W][CPL];
+    float bias[CPL];
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
+    for (int e = 0; e < CPL; ++e) {
         const int64_t c = active ? c0 + e : 0;
 #pragma unroll
         for (int k = 0; k < W; ++k)
@@ -206,20 +205,21 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
         bias[e] = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
     }
 
-    // Window of the H previous steps: win[i][e] = xx(t - H + i) for channel c0+e.
-    float win[W][EPV];
+    // win[i][e] = xx(t - H + i) for channel c0+e
+    float win[W][CPL];
     int32_t wid[W];
     const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
 #pragma unroll
     for (int i = 0; i < H; ++i) {
         const int64_t s = t0 - H + i;
-        u32x4 hv = vzero();
-        if (active && s >= 0) hv = vload(xb + s * xs2);
+        V hv;
+        hv.zero();
+        if (active && s >= 0) hv.template load<false>(xb + s * xs2);
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) win[i][e] = vget<T>(hv, e);
+        for (int e = 0; e < CPL; ++e) win[i][e] = hv.get(e);
         if (s < 0 && p.initial_states != nullptr && active) {
 #pragma unroll
-            for (int e = 0; e < EPV; ++e)
+            for (int e = 0; e < CPL; ++e)
                 win[i][e] = ld(static_cast<const T*>(p.initial_states),
                                b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
                                    (s + H) * p.initial_states_stride[2]);
@@ -228,23 +228,24 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
     }
 
     for (int64_t tb = t0; tb < t1; tb += U) {
-        u32x4 xv[U];
+        V xv[U];
         int32_t ids[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t t = tb + u;
-            xv[u] = (active && t < t1) ? vload_nt(xb + t * xs2) : vzero();
+            xv[u].zero();
+            if (active && t < t1) xv[u].template load<true>(xb + t * xs2);
             if constexpr (SEQ) ids[u] = (t < t1) ? sr[t * p.seq_idx_stride[1]] : -1;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int64_t t = tb + u;
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) win[H][e] = vget<T>(xv[u], e);
+            for (int e = 0; e < CPL; ++e) win[H][e] = xv[u].get(e);
             if constexpr (SEQ) wid[H] = ids[u];
-            float o[EPV];
+            float o[CPL];
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
+            for (int e = 0; e < CPL; ++e) {
                 float col[W], wc[W];
 #pragma unroll
                 for (int k = 0; k < W; ++k) { col[k] = win[k][e]; wc[k] = w[k][e]; }
@@ -257,11 +258,15 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
                 }
                 o[e] = acc;
             }
-            if (active && t < t1) vstore_nt(ob + t * os2, vpack<T>(o));
+            if (active && t < t1) {
+                V ov;
+                ov.set(o);
+                ov.template store<true>(ob + t * os2);
+            }
 #pragma unroll
             for (int i = 0; i < H; ++i) {
 #pragma unroll
-                for (int e = 0; e < EPV; ++e) win[i][e] = win[i + 1][e];
+                for (int e = 0; e < CPL; ++e) win[i][e] = win[i + 1][e];
                 if constexpr (SEQ) wid[i] = wid[i + 1];
             }
         }
@@ -273,7 +278,7 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
         for (int i = 0; i < H; ++i) {
             const int64_t s = L - H + i;
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
+            for (int e = 0; e < CPL; ++e) {
                 const float val = (s >= 0) ? ld(xb, s * xs2 + e) : 0.0f;
                 st(fs, (c0 + e) * p.final_states_stride[1] + i * p.final_states_stride[2], val);
             }
@@ -354,6 +359,11 @@ __global__ void __launch_bounds__(256) fwd_generic(const FwdArgs a) {
 
 namespace {
 
+// channel-last launch shape: channels per lane, steps per tile, steps in flight
+constexpr int kColsCPL = 4;
+constexpr int64_t kColsChunk = 64;
+constexpr int kColsU = 8;
+
 template <typename T>
 bool rows_vec_ok(const cc1d_fwd_params& p) {
     constexpr int64_t EPV = elems16<T>::value;
@@ -371,13 +381,15 @@ bool rows_vec_ok(const cc1d_fwd_params& p) {
     return true;
 }
 
-template <typename T>
+// channel-last with CPL-channel lanes: unit channel stride, CPL | dim and
+// every row start aligned to CPL elements
+template <typename T, int CPL>
 bool cols_vec_ok(const cc1d_fwd_params& p) {
-    constexpr int64_t EPV = elems16<T>::value;
+    constexpr int64_t NB = CPL * (int64_t)sizeof(T);
     if (p.x_stride[1] != 1 || p.out_stride[1] != 1) return false;
-    if (p.dim % EPV != 0) return false;
-    if (!aligned16(p.x) || !aligned16(p.out)) return false;
-    if (p.x_stride[0] % EPV || p.x_stride[2] % EPV || p.out_stride[0] % EPV || p.out_stride[2] % EPV) return false;
+    if (p.dim % CPL != 0) return false;
+    if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.out)) % NB) return false;
+    if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.out_stride[0] % CPL || p.out_stride[2] % CPL) return false;
     return true;
 }
 
@@ -413,15 +425,16 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         });
                     }
                 }
-                if (cols_vec_ok<T>(p)) {
-                    a.ngroups = ceil_div(p.dim / EPV, 64);
-                    a.chunk = 64;
+                constexpr int CPL = kColsCPL;
+                if (cols_vec_ok<T, CPL>(p)) {
+                    a.ngroups = ceil_div(p.dim / CPL, 64);
+                    a.chunk = kColsChunk;
                     a.nseg = ceil_div(p.seqlen, a.chunk);
                     a.n_items = p.batch * a.nseg * a.ngroups;
                     const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                     return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                         constexpr bool SEQ = decltype(qc)::value;
-                        fwd_cols_vec<T, W, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                        fwd_cols_vec<T, W, CPL, kColsU, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
                         return launch_status();
                     });
                 }
