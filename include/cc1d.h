@@ -22,11 +22,11 @@
  *
  * The entry points replace the reference's per-variant CPython extension
  * entry points (paths relative to /root/reference):
- *   cc1d_fwd           <- causal_conv1d_fwd_variant, src/causal_conv1d_mojo/fwd/variant.mojo:58-130,
+ *   cc1d_fwd           <- causal_conv1d_fwd_variant, src/causal_conv1d_mojo/fwd/variant.mojo:58-131,
  *                         fed by native_fwd's 29-int tuple, src/causal_conv1d_mojo/fwd/__init__.py:11-60
- *   cc1d_bwd           <- causal_conv1d_bwd_full_variant, src/causal_conv1d_mojo/bwd_full/variant.mojo:50-142,
+ *   cc1d_bwd           <- causal_conv1d_bwd_full_variant, src/causal_conv1d_mojo/bwd_full/variant.mojo:50-144,
  *                         fed by native_bwd_full, src/causal_conv1d_mojo/bwd_full/__init__.py:11-73
- *   cc1d_update        <- causal_conv1d_update_variant, src/causal_conv1d_mojo/update/variant.mojo:45-129,
+ *   cc1d_update        <- causal_conv1d_update_variant, src/causal_conv1d_mojo/update/variant.mojo:45-116,
  *                         fed by native_update, src/causal_conv1d_mojo/update/__init__.py:11-60
  *   cc1d_varlen_states <- causal_conv1d_varlen_states (pure torch in the reference),
  *                         src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-61
