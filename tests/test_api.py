@@ -10,7 +10,11 @@ running anything on the CPU.
 from __future__ import annotations
 
 import ast
+import importlib.util
 import inspect
+import shutil
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -178,3 +182,32 @@ def test_reference_functions_are_plain_torch(width):
 def test_modules_do_not_import_the_oracle():
     for mod in (_fn, _update):
         assert "oracle" not in inspect.getsource(mod)
+
+
+COMPAT = Path(__file__).resolve().parent.parent / "causal-conv1d-mojo_amd" / "compat"
+
+
+def test_compat_namespace_reexports_the_package():
+    """``import causal_conv1d`` (compat/src/causal_conv1d/__init__.py:24-48): same five names."""
+    sys.path.insert(0, str(COMPAT))
+    try:
+        sys.modules.pop("causal_conv1d", None)
+        import causal_conv1d
+    finally:
+        sys.path.remove(str(COMPAT))
+    assert sorted(causal_conv1d.__all__) == sorted(["__version__", "causal_conv1d_fn", "causal_conv1d_ref",
+                                                    "causal_conv1d_update", "causal_conv1d_update_ref"])
+    for name in causal_conv1d.__all__:
+        assert getattr(causal_conv1d, name) is getattr(cc, name)
+    assert not hasattr(causal_conv1d, "causal_conv1d_varlen_states")
+
+
+def test_compat_namespace_refuses_a_mixed_install(tmp_path):
+    """Upstream's interface module beside the shim's __init__ means two installs share the directory."""
+    pkg = tmp_path / "causal_conv1d"
+    pkg.mkdir()
+    shutil.copy(COMPAT / "causal_conv1d" / "__init__.py", pkg / "__init__.py")
+    (pkg / "causal_conv1d_interface.py").write_text("")
+    spec = importlib.util.spec_from_file_location("causal_conv1d_mixed", pkg / "__init__.py")
+    with pytest.raises(ImportError, match="causal_conv1d"):
+        spec.loader.exec_module(importlib.util.module_from_spec(spec))
