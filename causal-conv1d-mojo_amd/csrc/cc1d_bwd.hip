@@ -36,13 +36,46 @@ constexpr int kBwdColsCPL = 2;
 constexpr int64_t kBwdColsChunk = 64;
 constexpr int kBwdColsU = 4;
 
-// One wavefront-segment of row (b, c): writes dx (and dinitial_states) and
-// adds this segment's weight/bias-gradient partials into pw / pb. FULL: the
-// whole segment lies inside the row.
+// Registers of one wavefront-segment of a row: VPT 16-byte vectors of x and
+// dout per lane, plus the halos (lane 0: the vector of x before the segment;
+// lane 63: x and dout of the first vector after it).
+template <int VPT> struct RowTile {
+    u32x4 v[VPT], gv[VPT], h, xn, gn;
+};
+
+// Issue the loads of segment t0 of row (b, c). FULL: the whole segment lies
+// inside the row.
+template <typename T, int VPT, bool FULL>
+__device__ __forceinline__ void bwd_rows_load(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c, int32_t t0,
+                                              RowTile<VPT>& r) {
+    constexpr int EPV = elems16<T>::value;
+    constexpr int SEG = 64 * VPT * EPV;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t tn = t0 + SEG;  // first position of the next segment
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
+        r.v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
+        r.gv[j] = (FULL || t < L) ? vload_nt(gr + t) : vzero();
+    }
+    // halo vectors: wave-uniform reads at clamped (always valid) addresses
+    const u32x4 hv = vload_uniform(xr + (t0 > 0 ? t0 - EPV : 0));
+    const int32_t tq = tn < L ? tn : t0;
+    const u32x4 xv = vload_uniform(xr + tq), gq = vload_uniform(gr + tq);
+    r.h = (lane == 0 && t0 > 0) ? hv : vzero();
+    r.xn = (lane == 63 && tn < L) ? xv : vzero();
+    r.gn = (lane == 63 && tn < L) ? gq : vzero();
+}
+
+// One wavefront-segment of row (b, c) from its loaded tile: writes dx (and
+// dinitial_states) and adds this segment's weight/bias-gradient partials
+// into pw / pb.
 template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
-__device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0, const float* w, const float* wq, float bq, float* pw,
-                                                 float& pb) {
+__device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
+                                                 int32_t t0, const RowTile<VPT>& r, const float* w, const float* wq,
+                                                 float bq, float* pw, float& pb) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int SEG = 64 * VPT * EPV;
@@ -50,23 +83,10 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
     const int32_t L = (int32_t)p.seqlen;
     {
         const int32_t tn = t0 + SEG;  // first position of the next segment
-        const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
-        const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
         T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
-
-        u32x4 v[VPT], gv[VPT];
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int32_t t = t0 + (j * 64 + lane) * EPV;
-            v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
-            gv[j] = (FULL || t < L) ? vload_nt(gr + t) : vzero();
-        }
-        u32x4 h = vzero(), xn = vzero(), gn = vzero();
-        if (lane == 0 && t0 > 0) h = vload(xr - EPV + t0);
-        if (lane == 63 && tn < L) {
-            xn = vload(xr + tn);
-            gn = vload(gr + tn);
-        }
+        const auto& v = r.v;
+        const auto& gv = r.gv;
+        const u32x4 h = r.h, xn = r.xn, gn = r.gn;
 
         int32_t id[VPT][EPV];
         int32_t hid[H], nid[H];
@@ -90,15 +110,26 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
             }
         }
 
-        const bool use_init = p.initial_states != nullptr && t0 == 0 && lane == 0;
+        const bool init_row = p.initial_states != nullptr && t0 == 0;  // wave-uniform
+        const bool use_init = init_row && lane == 0;
         float hinit[H];
 #pragma unroll
-        for (int i = 0; i < H; ++i) {
-            hinit[i] = 0.0f;
-            if (use_init)
-                hinit[i] = ld(static_cast<const T*>(p.initial_states),
-                              b * p.initial_states_stride[0] + c * p.initial_states_stride[1] +
-                                  i * p.initial_states_stride[2]);
+        for (int i = 0; i < H; ++i) hinit[i] = 0.0f;
+        if (init_row) {
+            const T* is = static_cast<const T*>(p.initial_states) + b * p.initial_states_stride[0] +
+                          c * p.initial_states_stride[1];
+#pragma unroll
+            for (int i = 0; i < H; ++i) hinit[i] = ld_uniform(is + i * p.initial_states_stride[2]);
+        }
+        // dfinal_states of this row when the segment holds the row's end (wave-uniform)
+        float dfin[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) dfin[i] = 0.0f;
+        if (p.dfinal_states != nullptr && tn >= L) {
+            const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
+                           c * p.dfinal_states_stride[1];
+#pragma unroll
+            for (int i = 0; i < H; ++i) dfin[i] = ld_uniform(dfs + i * p.dfinal_states_stride[2]);
         }
 
         // ---- dpre for the owned positions + dweight/dbias partials ----
@@ -247,11 +278,8 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
             // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
             // here, so the W-1 tail positions are the end of the last vector.
             if (p.dfinal_states != nullptr && t + EPV == L) {
-                const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
-                               c * p.dfinal_states_stride[1];
 #pragma unroll
-                for (int i = EPV - H; i < EPV; ++i)
-                    o[i] = round_to<T>(o[i]) + ld(dfs, (H - EPV + i) * p.dfinal_states_stride[2]);
+                for (int i = EPV - H; i < EPV; ++i) o[i] = round_to<T>(o[i]) + dfin[H - EPV + i];
             }
             if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
         }
@@ -269,6 +297,15 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
             }
         }
     }
+}
+
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+__device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
+                                                 int32_t t0, const float* w, const float* wq, float bq, float* pw,
+                                                 float& pb) {
+    RowTile<VPT> r;
+    bwd_rows_load<T, VPT, FULL>(p, lane, b, c, t0, r);
+    bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
 }
 
 // One wavefront per block; item = (row, segment) with row = b * dim + c, in
@@ -294,8 +331,8 @@ __global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
     float w[W];
     const T* __restrict__ wr = static_cast<const T*>(p.weight) + (int64_t)c * p.weight_stride[0];
 #pragma unroll
-    for (int k = 0; k < W; ++k) w[k] = ld(wr, k * p.weight_stride[1]);
-    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), (int64_t)c * p.bias_stride) : 0.0f;
+    for (int k = 0; k < W; ++k) w[k] = ld_uniform(wr + k * p.weight_stride[1]);
+    const float bias = p.bias ? ld_uniform(static_cast<const T*>(p.bias) + (int64_t)c * p.bias_stride) : 0.0f;
     float wq[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) wq[k] = -kLog2e * w[k];

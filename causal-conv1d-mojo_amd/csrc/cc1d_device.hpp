@@ -157,6 +157,30 @@ template <typename T, int N> struct Lanes {
 };
 
 template <typename T> __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
+
+// Reads of wave-uniform addresses through the scalar data cache (constant
+// address space): for data that no wavefront writes during the kernel, such
+// as weights, bias and halo vectors of read-only inputs. Their completion is
+// tracked by lgkmcnt, so waiting for them never waits for the wavefront's
+// outstanding vector-memory reads.
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+typedef const __attribute__((address_space(4))) u32x4* const_u32x4_ptr;
+
+// Element at p (wave-uniform), widened to fp32: reads the aligned dword holding it.
+template <typename T> __device__ __forceinline__ float ld_uniform(const T* p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t d = *(const_u32_ptr)(a & ~(uintptr_t)3);
+    if constexpr (sizeof(T) == 4) {
+        return __uint_as_float(d);
+    } else {
+        const uint16_t h = (a & 2) ? (uint16_t)(d >> 16) : (uint16_t)(d & 0xffffu);
+        return to_f32(T{h});
+    }
+}
+// 16-byte vector at the wave-uniform, 16-byte aligned address p.
+template <typename T> __device__ __forceinline__ u32x4 vload_uniform(const T* p) {
+    return *(const_u32x4_ptr)reinterpret_cast<uintptr_t>(p);
+}
 template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 
 // SiLU = x * sigmoid(x), as x * rcp(1 + exp(-x)) in fp32.
