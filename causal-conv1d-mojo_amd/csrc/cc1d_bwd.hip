@@ -16,8 +16,8 @@
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
 //                   fwd_rows_vec (one wavefront per block).
-//   bwd_cols_vec -- channel-last (unit channel stride); lanes own adjacent
-//                   channels and walk a tile of time steps.
+//   bwd_cl       -- channel-last (unit channel stride); a lane owns 4 bytes of
+//                   adjacent channels, a wavefront a tile of time steps.
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
 #include "cc1d_internal.hpp"
 
@@ -25,16 +25,15 @@ namespace cc1d {
 
 struct BwdArgs {
     cc1d_bwd_params p;
-    int64_t nseg;     // segments / tiles / chunks per row
-    int64_t n_items;  // rows_vec: (row, segment) items; cols: wavefronts; generic: threads
-    int64_t chunk;    // cols / generic: time steps per item
-    int64_t groups;   // cols: channel groups of 64 * CPL
+    int64_t nseg;     // rows_vec: segments per row; cl: tile groups per row; generic: chunks per row
+    int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
+    int64_t chunk;    // cl: time steps per tile; generic: time steps per thread
+    int64_t groups;   // cl: channel groups of 64 * CPL
 };
 
-// channel-last launch shape: channels per lane, steps per tile, steps in flight
-constexpr int kBwdColsCPL = 2;
-constexpr int64_t kBwdColsChunk = 64;
-constexpr int kBwdColsU = 4;
+// channel-last launch shape: time steps per wavefront tile, tiles per block
+constexpr int kClTS = 16;
+constexpr int kClWPB = 4;
 
 // Registers of one wavefront-segment of a row: VPT 16-byte vectors of x and
 // dout per lane, plus the halos (lane 0: the vector of x before the segment;
@@ -360,243 +359,16 @@ __global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
         unsafeAtomicAdd(p.dbias_acc + (int64_t)c * p.dbias_acc_stride, mine);
 }
 
-// Wavefront-scope barrier for an LDS exchange between the lanes of one
-// wavefront (orders this wavefront's LDS writes before its reads).
-__device__ __forceinline__ void wave_lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Channel-last backward: x / dout / dx have unit channel stride. Work item =
-// (b, tile of `chunk` steps, group of 64*CPL channels), group fastest; a
-// lane owns CPL adjacent channels. The wavefront walks s = t0 .. t1+W-2:
-// dpre[s] needs x[s-W+1 .. s] (register window) and dout[s]; once dpre[s] is
-// known, dx[s-W+1] is complete. The W-1 steps past the tile are recomputed
-// (they are the next tile's first steps). Loads are double-buffered: the
-// next U steps are in flight while the current U are computed. seq_idx is
-// one value per step, identical for every lane. At the end the lanes'
-// weight/bias-gradient partials are transposed through LDS so that the fp32
-// atomic adds of a wavefront land on consecutive addresses.
-template <typename T, int W, int CPL, int U, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(256) bwd_cols_vec(const BwdArgs a) {
-    constexpr int H = W - 1;
-    constexpr int NR = 64 * CPL;  // channels per wavefront
-    static_assert(U >= H, "the first step group must cover the W-1 initial positions");
-    using V = Lanes<T, CPL>;
-    __shared__ float red[4][NR * (W + 1)];
-    const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t item = uniform((int64_t)blockIdx.x * 4 + wave);
-    if (item >= a.n_items) return;
-    const int64_t g = item % a.groups;
-    const int64_t rest = item / a.groups;
-    const int64_t tile = rest % a.nseg;
-    const int64_t b = rest / a.nseg;
-    const int64_t cw0 = g * NR;  // first channel of this wavefront
-    const int64_t c0 = cw0 + lane * CPL;
-    const bool active = c0 < p.dim;
-    const int64_t L = p.seqlen;
-    const int64_t t0 = tile * a.chunk;
-    const int64_t t1 = (t0 + a.chunk < L) ? t0 + a.chunk : L;
-    const int64_t send = (t1 + H < L) ? t1 + H : L;  // positions whose dpre is needed
-    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
-    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
-    T* __restrict__ db = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
-    const int64_t xs2 = p.x_stride[2], gs2 = p.dout_stride[2], ds2 = p.dx_stride[2];
-    const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
-
-    float w[W][CPL], wq[W][CPL], bq[CPL];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-        const int64_t c = active ? c0 + e : 0;
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
-            wq[k][e] = -kLog2e * w[k][e];
-        }
-        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
-    }
-
-    // windows over positions s-H .. s
-    float xw[W][CPL], dw[W][CPL];
-    int32_t iw[W];
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-        const int64_t s = t0 - H + i;
-        V hv;
-        hv.zero();
-        if (active && s >= 0) hv.template load<false>(xb + s * xs2);
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            xw[i][e] = hv.get(e);
-            dw[i][e] = 0.0f;
-        }
-        if (s < 0 && p.initial_states != nullptr && active) {
-#pragma unroll
-            for (int e = 0; e < CPL; ++e)
-                xw[i][e] = ld(static_cast<const T*>(p.initial_states),
-                              b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
-                                  (s + H) * p.initial_states_stride[2]);
-        }
-        iw[i] = (SEQ && s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
-    }
-    float pw[W][CPL], pb[CPL], dfirst[H > 0 ? H : 1][CPL];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-        pb[e] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < W; ++k) pw[k][e] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < H; ++i) dfirst[i][e] = 0.0f;
-    }
-    const int64_t m = (H < L) ? H : L;  // dfinal tail length
-
-    auto load_group = [&](V* xv, V* gv, int32_t* ids, int64_t sb) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t s = sb + u;
-            xv[u].zero();
-            gv[u].zero();
-            if (active && s < send) {
-                xv[u].template load<true>(xb + s * xs2);
-                gv[u].template load<true>(gb + s * gs2);
-            }
-            ids[u] = (SEQ && s < send) ? sr[s * p.seq_idx_stride[1]] : -1;
-        }
-    };
-    auto run_group = [&](const V* xv, const V* gv, const int32_t* ids, int64_t sb) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t s = sb + u;
-            if (s >= t1 + H) break;
-            const bool in = s < L;
-            iw[H] = ids[u];
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                xw[H][e] = xv[u].get(e);
-                const float gval = gv[u].get(e);
-                float d = gval;
-                if constexpr (SILU) {
-                    float q = bq[e];
-#pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if (!SEQ || iw[k] == iw[H]) q = __builtin_fmaf(wq[k][e], xw[k][e], q);
-                    }
-                    d = silu_bwd_q(gval, q);
-                }
-                if (!in || (SEQ && iw[H] < 0)) d = 0.0f;
-                dw[H][e] = d;
-                if (s < t1) {
-                    pb[e] += d;
-#pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if (!SEQ || iw[k] == iw[H]) pw[k][e] = __builtin_fmaf(d, xw[k][e], pw[k][e]);
-                    }
-                }
-            }
-            if (sb == 0 && u < H) {  // dpre[0 .. W-2] for dinitial_states (t0 == 0)
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) dfirst[u < H ? u : 0][e] = dw[H][e];
-            }
-            const int64_t q = s - H;  // dx[q] is complete
-            if (q >= t0) {
-                float o[CPL];
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    float acc = 0.0f;
-#pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if (!SEQ || iw[k] == iw[0]) acc = __builtin_fmaf(w[H - k][e], dw[k][e], acc);
-                    }
-                    if (p.dfinal_states != nullptr && q >= L - m && active)
-                        acc = round_to<T>(acc) + ld(static_cast<const T*>(p.dfinal_states),
-                                                    b * p.dfinal_states_stride[0] + (c0 + e) * p.dfinal_states_stride[1] +
-                                                        (q - L + H) * p.dfinal_states_stride[2]);
-                    o[e] = acc;
-                }
-                if (active) {
-                    V ov;
-                    ov.set(o);
-                    ov.template store<true>(db + q * ds2);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    xw[i][e] = xw[i + 1][e];
-                    dw[i][e] = dw[i + 1][e];
-                }
-                iw[i] = iw[i + 1];
-            }
-        }
-    };
-    V xa[U], ga[U], xc[U], gc[U];
-    int32_t ia[U], ic[U];
-    load_group(xa, ga, ia, t0);
-    for (int64_t sb = t0; sb < t1 + H; sb += 2 * U) {
-        load_group(xc, gc, ic, sb + U);
-        run_group(xa, ga, ia, sb);
-        load_group(xa, ga, ia, sb + 2 * U);
-        if (sb + U < t1 + H) run_group(xc, gc, ic, sb + U);
-    }
-
-    if (p.dinitial_states != nullptr && t0 == 0 && active) {
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
-                    (c0 + e) * p.dinitial_states_stride[1];
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], dfirst[i - k][e], acc);
-                st(di, i * p.dinitial_states_stride[2], acc);
-            }
-        }
-    }
-
-    // ---- weight / bias gradient: transpose through LDS, then consecutive atomics ----
-    float* r = red[wave];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-        for (int k = 0; k < W; ++k) r[(lane * CPL + e) * W + k] = pw[k][e];
-        r[NR * W + lane * CPL + e] = pb[e];
-    }
-    wave_lds_barrier();
-#pragma unroll
-    for (int j = 0; j < CPL * W; ++j) {
-        const int idx = j * 64 + lane;  // (channel, tap) pair, taps fastest
-        const int64_t c = cw0 + idx / W;
-        if (c < p.dim)
-            unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + (idx % W) * p.dweight_acc_stride[1], r[idx]);
-    }
-    if (p.dbias_acc != nullptr) {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int idx = j * 64 + lane;
-            const int64_t c = cw0 + idx;
-            if (c < p.dim) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, r[NR * W + idx]);
-        }
-    }
-}
-
+// One channel c of batch b over steps [t0, t1), any strides: writes dx (and
+// dinitial_states when t0 == 0) and returns the chunk's weight/bias-gradient
+// partials in pw / pb. Windows of the previous W-1 positions are rolled in
+// registers; the step loop is not unrolled, so the register footprint is
+// small.
 template <typename T, int W, bool SILU>
-__global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
+__device__ __forceinline__ void bwd_chunk(const cc1d_bwd_params& p, int64_t b, int64_t c, int64_t t0, int64_t t1,
+                                          float* pw, float& pb) {
     constexpr int H = W - 1;
-    const cc1d_bwd_params& p = a.p;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.n_items) return;
-    const int64_t c = idx % p.dim;
-    const int64_t rest = idx / p.dim;
-    const int64_t ch = rest % a.nseg;
-    const int64_t b = rest / a.nseg;
     const int64_t L = p.seqlen;
-    const int64_t t0 = ch * a.chunk;
-    const int64_t t1 = (t0 + a.chunk < L) ? t0 + a.chunk : L;
     const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
     const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
     T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
@@ -622,10 +394,9 @@ __global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
         iw[i] = (sr != nullptr && s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
         dw[i] = 0.0f;
     }
-    float pw[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) pw[k] = 0.0f;
-    float pb = 0.0f;
+    pb = 0.0f;
     float dfirst[H];
 #pragma unroll
     for (int i = 0; i < H; ++i) dfirst[i] = 0.0f;
@@ -687,6 +458,270 @@ __global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
             st(di, i * p.dinitial_states_stride[2], acc);
         }
     }
+}
+
+// ---- channel-last (unit channel stride) backward, tiled ----------------
+//
+// A lane owns CPL adjacent channels and a wavefront one tile of TS time
+// steps of 64 * CPL channels. The tile's registers hold x rows
+// t0-W+1 .. t0+TS+W-2 and dout rows t0 .. t0+TS+W-2; dpre is recomputed for
+// t0 .. t0+TS+W-2 (the last W-1 belong to the next tile and only feed dx
+// here). Index arithmetic is 32-bit inside a batch (the launcher checks the
+// ranges).
+
+template <typename T, int W, int CPL, int TS> struct ClTile {
+    static constexpr int H = W - 1;
+    static constexpr int NX = TS + 2 * H;  // x rows: position t0 - H + i
+    static constexpr int ND = TS + H;      // dout / dpre rows: position t0 + j
+    Lanes<T, CPL> xv[NX], gv[ND];
+};
+
+template <int W, int CPL> struct ClPartials {
+    float pw[W][CPL];
+    float pb[CPL];
+};
+
+// Issue the loads of the tile at t0 (rows outside the sequence are zero;
+// rows before 0 come from initial_states when given).
+template <typename T, int W, int CPL, int TS>
+__device__ __forceinline__ void cl_bwd_load(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0, bool active,
+                                            ClTile<T, W, CPL, TS>& r) {
+    using Tile = ClTile<T, W, CPL, TS>;
+    constexpr int H = W - 1;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
+    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
+    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
+#pragma unroll
+    for (int i = 0; i < Tile::NX; ++i) {
+        const int32_t s = t0 - H + i;
+        r.xv[i].zero();
+        if (active && s >= 0 && s < L) r.xv[i].template load<false>(xb + s * xs2);
+    }
+#pragma unroll
+    for (int j = 0; j < Tile::ND; ++j) {
+        const int32_t t = t0 + j;
+        r.gv[j].zero();
+        if (active && t < L) r.gv[j].template load<false>(gb + t * gs2);
+    }
+    if (p.initial_states != nullptr && t0 < H && active) {
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const int32_t s = t0 - H + i;
+            if (s < 0) {
+                float f[CPL];
+#pragma unroll
+                for (int e = 0; e < CPL; ++e)
+                    f[e] = ld(static_cast<const T*>(p.initial_states),
+                              b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
+                                  (s + H) * p.initial_states_stride[2]);
+                r.xv[i].set(f);
+            }
+        }
+    }
+}
+
+// seq_idx of the tile's x-row window: lane i < NX reads position t0 - H + i
+// (clamped address, -1 outside the row), so the reads are one vector load.
+template <int NX>
+__device__ __forceinline__ int32_t cl_window_id(const int32_t* sr, int32_t ss1, int32_t L, int32_t t0, int32_t H,
+                                                int lane) {
+    static_assert(NX <= 64, "the id window must fit in one wavefront");
+    const int32_t s = t0 - H + lane;
+    const int32_t v = sr[(s < 0 ? 0 : (s < L ? s : L - 1)) * ss1];
+    return (s >= 0 && s < L) ? v : -1;
+}
+
+// dpre, dx (+ dfinal tail, dinitial_states) and the weight/bias-gradient
+// partials of a loaded tile. G: apply the seq_idx equality gate with the
+// window ids id[0 .. NX-1] (wave-uniform).
+template <typename T, int W, int CPL, int TS, bool SILU, bool G>
+__device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
+                                               bool active, const ClTile<T, W, CPL, TS>& r, const int32_t* id,
+                                               ClPartials<W, CPL>& out) {
+    using Tile = ClTile<T, W, CPL, TS>;
+    constexpr int H = W - 1;
+    constexpr int ND = Tile::ND;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t ds2 = (int32_t)p.dx_stride[2];
+    T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
+
+    float w[W][CPL], wq[W][CPL], bq[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        const int64_t c = active ? c0 + e : 0;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+            wq[k][e] = -kLog2e * w[k][e];
+        }
+        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
+    }
+
+    float dp[ND][CPL];
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+        const int32_t t = t0 + j;
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            const float gval = r.gv[j].get(e);
+            float d = gval;
+            if constexpr (SILU) {
+                float q = bq[e];
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (!G || id[j + k] == id[j + H]) q = __builtin_fmaf(wq[k][e], r.xv[j + k].get(e), q);
+                d = silu_bwd_q(gval, q);
+            }
+            if (t >= L) d = 0.0f;
+            if constexpr (G) {
+                if (id[j + H] < 0) d = 0.0f;
+            }
+            dp[j][e] = d;
+            if (j < TS) {
+                out.pb[e] += d;
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (!G || id[j + k] == id[j + H]) out.pw[k][e] = __builtin_fmaf(d, r.xv[j + k].get(e), out.pw[k][e]);
+            }
+        }
+    }
+    const int32_t m = H < L ? H : L;  // dfinal tail length
+#pragma unroll
+    for (int j = 0; j < TS; ++j) {
+        const int32_t t = t0 + j;
+        float o[CPL];
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < W; ++k)
+                if (!G || id[j + H + k] == id[j + H]) acc = __builtin_fmaf(w[H - k][e], dp[j + k][e], acc);
+            o[e] = acc;
+        }
+        if (p.dfinal_states != nullptr && t >= L - m && t < L && active) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e)
+                o[e] = round_to<T>(o[e]) + ld(static_cast<const T*>(p.dfinal_states),
+                                              b * p.dfinal_states_stride[0] + (c0 + e) * p.dfinal_states_stride[1] +
+                                                  (t - L + H) * p.dfinal_states_stride[2]);
+        }
+        if (active && t < L) {
+            Lanes<T, CPL> ov;
+            ov.set(o);
+            ov.template store<true>(dxb + t * ds2);
+        }
+    }
+    // dinitial_states (bwd_full_cpu/kernel.mojo:210-219)
+    if (p.dinitial_states != nullptr && t0 == 0 && active) {
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
+                    (c0 + e) * p.dinitial_states_stride[1];
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], dp[i - k][e], acc);
+                st(di, i * p.dinitial_states_stride[2], acc);
+            }
+        }
+    }
+}
+
+// Kernel: the WPB wavefronts of a block take WPB consecutive tiles of the
+// same channels; their weight/bias-gradient partials are summed through LDS
+// and the block adds the sums with fp32 atomics on consecutive addresses.
+// Block order: channel group fastest, then tile group, then batch. With
+// seq_idx, a tile whose in-sequence rows all carry one id (>= 0) takes the
+// ungated path; rows outside [0, L) hold zeros (seq_idx excludes
+// initial_states) and feed only zeroed terms, so they do not count.
+template <typename T, int W, int CPL, int TS, int WPB, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
+    using Tile = ClTile<T, W, CPL, TS>;
+    constexpr int H = W - 1;
+    constexpr int NC = 64 * CPL;  // channels per wavefront
+    __shared__ float red[WPB][NC * (W + 1)];
+    const cc1d_bwd_params& p = a.p;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t ngroups = (uint32_t)a.groups, ntgroups = (uint32_t)a.nseg;
+    const uint32_t g = blockIdx.x % ngroups;
+    const uint32_t rest = blockIdx.x / ngroups;
+    const uint32_t tg = rest % ntgroups;
+    const uint32_t b = rest / ntgroups;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t t0 = (int32_t)uniform32((tg * WPB + wave) * TS);
+    const int32_t cw0 = (int32_t)(g * NC);
+    const int32_t c0 = cw0 + lane * CPL;
+    const bool active = c0 < (int32_t)p.dim;
+
+    ClPartials<W, CPL> part;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        part.pb[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) part.pw[k][e] = 0.0f;
+    }
+    if (t0 < L) {  // tiles past the end only join the block reduction
+        Tile r;
+        cl_bwd_load<T, W, CPL, TS>(p, b, t0, c0, active, r);
+        bool one_id = true;
+        int32_t id[Tile::NX];
+        if constexpr (SEQ) {
+            const int32_t s = t0 - H + lane;
+            const int32_t lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0],
+                                                       (int32_t)p.seq_idx_stride[1], L, t0, H, lane);
+            const int32_t id_cur = __builtin_amdgcn_readlane(lid, H);
+            one_id = id_cur >= 0 && __ballot(lane < Tile::NX && s >= 0 && s < L && lid != id_cur) == 0;
+#pragma unroll
+            for (int i = 0; i < Tile::NX; ++i) id[i] = __builtin_amdgcn_readlane(lid, i);
+        }
+        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU, false>(p, b, t0, c0, active, r, id, part);
+        else if constexpr (SEQ) cl_bwd_compute<T, W, CPL, TS, SILU, true>(p, b, t0, c0, active, r, id, part);
+    }
+
+    // ---- weight / bias gradient: sum the block's tiles in LDS, then
+    //      consecutive fp32 atomics ----
+    float* rr = red[wave];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+#pragma unroll
+        for (int k = 0; k < W; ++k) rr[(lane * CPL + e) * W + k] = part.pw[k][e];
+        rr[NC * W + lane * CPL + e] = part.pb[e];
+    }
+    __syncthreads();
+    constexpr int NE = NC * (W + 1);
+    for (int idx = threadIdx.x; idx < NE; idx += 64 * WPB) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < WPB; ++q) sum += red[q][idx];
+        if (idx < NC * W) {
+            const int32_t c = cw0 + idx / W;
+            if (c < (int32_t)p.dim)
+                unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + (idx % W) * p.dweight_acc_stride[1], sum);
+        } else if (p.dbias_acc != nullptr) {
+            const int32_t c = cw0 + (idx - NC * W);
+            if (c < (int32_t)p.dim) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, sum);
+        }
+    }
+}
+
+template <typename T, int W, bool SILU>
+__global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
+    constexpr int H = W - 1;
+    const cc1d_bwd_params& p = a.p;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n_items) return;
+    const int64_t c = idx % p.dim;
+    const int64_t rest = idx / p.dim;
+    const int64_t ch = rest % a.nseg;
+    const int64_t b = rest / a.nseg;
+    const int64_t t0 = ch * a.chunk;
+    const int64_t t1 = (t0 + a.chunk < p.seqlen) ? t0 + a.chunk : p.seqlen;
+    float pw[W], pb;
+    bwd_chunk<T, W, SILU>(p, b, c, t0, t1, pw, pb);
+    (void)H;
 #pragma unroll
     for (int k = 0; k < W; ++k)
         unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], pw[k]);
@@ -714,8 +749,10 @@ bool rows_vec_ok(const cc1d_bwd_params& p) {
     return true;
 }
 
+// channel-last tiles: unit channel stride, CPL | dim, rows aligned to the
+// CPL-channel lane vector, 32-bit positions inside a batch
 template <typename T, int CPL>
-bool cols_vec_ok(const cc1d_bwd_params& p) {
+bool cl_ok(const cc1d_bwd_params& p) {
     constexpr int64_t NB = CPL * (int64_t)sizeof(T);
     if (p.x_stride[1] != 1 || p.dout_stride[1] != 1 || p.dx_stride[1] != 1) return false;
     if (p.dim % CPL != 0) return false;
@@ -725,6 +762,12 @@ bool cols_vec_ok(const cc1d_bwd_params& p) {
     if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.dout_stride[0] % CPL || p.dout_stride[2] % CPL ||
         p.dx_stride[0] % CPL || p.dx_stride[2] % CPL)
         return false;
+    const int64_t span = p.seqlen + kClTS + 16;  // furthest row a tile touches
+    const int64_t lim = (int64_t)1 << 31;
+    if (p.dim >= lim || span * p.x_stride[2] >= lim || span * p.dout_stride[2] >= lim || span * p.dx_stride[2] >= lim)
+        return false;
+    if (p.seq_idx != nullptr && span * p.seq_idx_stride[1] >= lim) return false;
+    if (p.batch * ceil_div(p.dim / CPL, 64) * ceil_div(ceil_div(p.seqlen, kClTS), kClWPB) >= lim) return false;
     return true;
 }
 
@@ -759,17 +802,16 @@ int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
                         });
                     }
                 }
-                constexpr int CPL = kBwdColsCPL;
-                if (cols_vec_ok<T, CPL>(p)) {
+                constexpr int CPL = 4 / (int)sizeof(T);
+                if (cl_ok<T, CPL>(p)) {
                     a.groups = ceil_div(p.dim / CPL, 64);
-                    a.chunk = kBwdColsChunk;
-                    a.nseg = ceil_div(p.seqlen, a.chunk);
-                    a.n_items = p.batch * a.nseg * a.groups;
-                    const dim3 grid((unsigned)ceil_div(a.n_items, 4));
+                    a.chunk = kClTS;
+                    a.nseg = ceil_div(ceil_div(p.seqlen, kClTS), kClWPB);  // tile groups per row
+                    a.n_items = 0;
+                    const dim3 grid((unsigned)(p.batch * a.groups * a.nseg));
                     return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                         constexpr bool SEQ = decltype(qc)::value;
-                        bwd_cols_vec<T, W, CPL, (kBwdColsU > W - 1 ? kBwdColsU : W - 1), SILU, SEQ>
-                            <<<grid, 256, 0, stream>>>(a);
+                        bwd_cl<T, W, CPL, kClTS, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
                         return launch_status();
                     });
                 }

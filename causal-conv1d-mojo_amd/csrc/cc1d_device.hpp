@@ -177,6 +177,9 @@ template <typename T> __device__ __forceinline__ float ld_uniform(const T* p) {
         return to_f32(T{h});
     }
 }
+__device__ __forceinline__ int32_t ld_uniform(const int32_t* p) {
+    return (int32_t)*(const_u32_ptr)reinterpret_cast<uintptr_t>(p);
+}
 // 16-byte vector at the wave-uniform, 16-byte aligned address p.
 template <typename T> __device__ __forceinline__ u32x4 vload_uniform(const T* p) {
     return *(const_u32x4_ptr)reinterpret_cast<uintptr_t>(p);

@@ -15,10 +15,11 @@
 //                    halo before a vector comes from the neighbouring lane
 //                    (ds_bpermute); only lane 0 of a segment reads one extra
 //                    vector from global memory. No LDS, no barriers.
-//   fwd_cols_vec  -- rows contiguous along channels (channel-last). A lane owns
-//                    EPV adjacent channels (one 16-byte vector per time step)
-//                    and walks a tile of time steps with a register window of
-//                    the previous W-1 steps; seq_idx is wave-uniform here.
+//   fwd_cl        -- rows contiguous along channels (channel-last). A lane owns
+//                    4 bytes of adjacent channels, a wavefront a tile of 16
+//                    time steps (plus W-1 halo rows) of 64 lanes' channels,
+//                    all loaded before any arithmetic; seq_idx is
+//                    wave-uniform here.
 //   fwd_generic   -- any strides / alignment; one thread per
 //                    (b, c, chunk of time), lanes on adjacent channels.
 #include "cc1d_internal.hpp"
@@ -27,10 +28,10 @@ namespace cc1d {
 
 struct FwdArgs {
     cc1d_fwd_params p;
-    int64_t nseg;     // segments (vec) or chunks (generic) per row
+    int64_t nseg;     // segments (rows_vec), tiles (cl) or chunks (generic) per row
     int64_t n_items;  // work items: segments / tiles / threads
-    int64_t chunk;    // time steps per item (generic / cols)
-    int64_t ngroups;  // channel groups (cols)
+    int64_t chunk;    // time steps per item (cl / generic)
+    int64_t ngroups;  // channel groups (cl)
 };
 
 // One wavefront-segment of one row. FULL: the whole segment lies inside the
@@ -167,35 +168,61 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
     else fwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0);
 }
 
-// Channel-last: x[b, c, t] at b*xs0 + c + t*xs2 (unit channel stride).
-// Work item = (b, tile of `chunk` steps, group of 64*CPL channels), group
-// fastest. A lane owns CPL adjacent channels (one CPL-element vector per
-// time step) and walks its tile with a register window of the previous W-1
-// steps; the U loads of a step group are issued before their arithmetic.
-// seq_idx is one value per time step here, identical for every lane.
-template <typename T, int W, int CPL, int U, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
+// Channel-last (unit channel stride), tiled: a lane owns CPL adjacent
+// channels (one CPL-element vector per time step); a wavefront covers
+// 64 * CPL channels of a tile of TS time steps and issues the loads of all
+// TS + W - 1 rows of its window (the W-1 halo rows before the tile included)
+// before any arithmetic. seq_idx is one value per time step, the same for
+// every lane: it is read through the scalar cache, and a tile whose window
+// holds one sequence id (>= 0) takes the ungated path. Item order: channel
+// group fastest, then tile, then batch. Index arithmetic is 32-bit inside a
+// batch (the launcher checks the ranges).
+template <typename T, int W, int CPL, int TS, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(256) fwd_cl(const FwdArgs a) {
     constexpr int H = W - 1;
+    constexpr int NR = TS + H;
     using V = Lanes<T, CPL>;
     const cc1d_fwd_params& p = a.p;
     const int lane = threadIdx.x & 63;
-    const int64_t item = uniform((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6));
-    if (item >= a.n_items) return;
-    const int64_t g = item % a.ngroups;
-    const int64_t rest = item / a.ngroups;
-    const int64_t tile = rest % a.nseg;
-    const int64_t b = rest / a.nseg;
-    const int64_t c0 = (g * 64 + lane) * CPL;
-    const bool active = c0 < p.dim;
-    const int64_t L = p.seqlen;
-    const int64_t t0 = tile * a.chunk;
-    const int64_t t1 = (t0 + a.chunk < L) ? t0 + a.chunk : L;
-    const int64_t xs2 = p.x_stride[2], os2 = p.out_stride[2];
+    const uint32_t item = uniform32(blockIdx.x * 4 + (threadIdx.x >> 6));
+    if (item >= (uint32_t)a.n_items) return;
+    const uint32_t ngroups = (uint32_t)a.ngroups, ntiles = (uint32_t)a.nseg;
+    const uint32_t g = item % ngroups;
+    const uint32_t rest = item / ngroups;
+    const uint32_t tile = rest % ntiles;
+    const uint32_t b = rest / ntiles;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t c0 = (int32_t)((g * 64 + lane) * CPL);
+    const bool active = c0 < (int32_t)p.dim;
+    const int32_t t0 = (int32_t)(tile * TS);
+    const int32_t xs2 = (int32_t)p.x_stride[2], os2 = (int32_t)p.out_stride[2];
     const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
     T* __restrict__ ob = static_cast<T*>(p.out) + b * p.out_stride[0] + c0;
 
-    float w[W][CPL];
-    float bias[CPL];
+    V xv[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int32_t s = t0 - H + i;
+        xv[i].zero();
+        if (active && s >= 0 && s < L) xv[i].template load<false>(xb + s * xs2);
+    }
+    if (p.initial_states != nullptr && t0 < H && active) {
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const int32_t s = t0 - H + i;
+            if (s < 0) {
+                float f[CPL];
+#pragma unroll
+                for (int e = 0; e < CPL; ++e)
+                    f[e] = ld(static_cast<const T*>(p.initial_states),
+                              b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
+                                  (s + H) * p.initial_states_stride[2]);
+                xv[i].set(f);
+            }
+        }
+    }
+
+    float w[W][CPL], bias[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
         const int64_t c = active ? c0 + e : 0;
@@ -205,83 +232,75 @@ __global__ void __launch_bounds__(256) fwd_cols_vec(const FwdArgs a) {
         bias[e] = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
     }
 
-    // win[i][e] = xx(t - H + i) for channel c0+e
-    float win[W][CPL];
-    int32_t wid[W];
-    const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
+    int32_t id[NR];
+    bool one_id = true;
+    if constexpr (SEQ) {
+        // lane i < NR reads the id of position t0 - H + i (clamped address,
+        // -1 outside the row); the window's ids then reach every lane through
+        // readlane, with no dependent scalar reads.
+        static_assert(NR <= 64, "the id window must fit in one wavefront");
+        const int32_t* sr = p.seq_idx + b * p.seq_idx_stride[0];
+        const int32_t s = t0 - H + lane;
+        int32_t lid = sr[(s < 0 ? 0 : (s < L ? s : L - 1)) * (int32_t)p.seq_idx_stride[1]];
+        if (s < 0 || s >= L) lid = -1;
+        const int32_t id_cur = __builtin_amdgcn_readlane(lid, H);
+        // rows outside [0, L) hold zeros (seq_idx excludes initial_states) or
+        // feed outputs that are not stored, so they do not break a single-id window
+        one_id = id_cur >= 0 && __ballot(lane < NR && s >= 0 && s < L && lid != id_cur) == 0;
 #pragma unroll
-    for (int i = 0; i < H; ++i) {
-        const int64_t s = t0 - H + i;
-        V hv;
-        hv.zero();
-        if (active && s >= 0) hv.template load<false>(xb + s * xs2);
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) win[i][e] = hv.get(e);
-        if (s < 0 && p.initial_states != nullptr && active) {
-#pragma unroll
-            for (int e = 0; e < CPL; ++e)
-                win[i][e] = ld(static_cast<const T*>(p.initial_states),
-                               b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
-                                   (s + H) * p.initial_states_stride[2]);
-        }
-        if constexpr (SEQ) wid[i] = (s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
+        for (int i = 0; i < NR; ++i) id[i] = __builtin_amdgcn_readlane(lid, i);
     }
 
-    for (int64_t tb = t0; tb < t1; tb += U) {
-        V xv[U];
-        int32_t ids[U];
+    auto emit = [&](auto gated) {
+        constexpr bool G = decltype(gated)::value;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t t = tb + u;
-            xv[u].zero();
-            if (active && t < t1) xv[u].template load<true>(xb + t * xs2);
-            if constexpr (SEQ) ids[u] = (t < t1) ? sr[t * p.seq_idx_stride[1]] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t t = tb + u;
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) win[H][e] = xv[u].get(e);
-            if constexpr (SEQ) wid[H] = ids[u];
+        for (int u = 0; u < TS; ++u) {
+            const int32_t t = t0 + u;
             float o[CPL];
 #pragma unroll
             for (int e = 0; e < CPL; ++e) {
                 float col[W], wc[W];
 #pragma unroll
-                for (int k = 0; k < W; ++k) { col[k] = win[k][e]; wc[k] = w[k][e]; }
+                for (int k = 0; k < W; ++k) {
+                    col[k] = xv[u + k].get(e);
+                    wc[k] = w[k][e];
+                }
                 float acc;
-                if constexpr (SEQ) acc = conv_taps_gated<W>(bias[e], wc, col, wid);
+                if constexpr (G) acc = conv_taps_gated<W>(bias[e], wc, col, id + u);
                 else acc = conv_taps<W>(bias[e], wc, col);
                 if constexpr (SILU) acc = silu(acc);
-                if constexpr (SEQ) {
-                    if (wid[H] < 0) acc = 0.0f;
+                if constexpr (G) {
+                    if (id[u + H] < 0) acc = 0.0f;
                 }
                 o[e] = acc;
             }
-            if (active && t < t1) {
+            if (active && t < L) {
                 V ov;
                 ov.set(o);
                 ov.template store<true>(ob + t * os2);
             }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) win[i][e] = win[i + 1][e];
-                if constexpr (SEQ) wid[i] = wid[i + 1];
-            }
         }
-    }
+    };
+    if (!SEQ || one_id) emit(std::false_type{});
+    else if constexpr (SEQ) emit(std::true_type{});
 
-    if (p.final_states_out != nullptr && active && t1 == L) {
+    if (p.final_states_out != nullptr && active && t0 + TS >= L) {
         T* fs = static_cast<T*>(p.final_states_out) + b * p.final_states_stride[0];
 #pragma unroll
         for (int i = 0; i < H; ++i) {
-            const int64_t s = L - H + i;
+            const int32_t r = L - t0 + i;  // register row of position L - H + i
+            float f[CPL];
 #pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                const float val = (s >= 0) ? ld(xb, s * xs2 + e) : 0.0f;
-                st(fs, (c0 + e) * p.final_states_stride[1] + i * p.final_states_stride[2], val);
-            }
+            for (int e = 0; e < CPL; ++e) f[e] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NR; ++q)
+                if (q == r && L - H + i >= 0) {
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) f[e] = xv[q].get(e);
+                }
+#pragma unroll
+            for (int e = 0; e < CPL; ++e)
+                st(fs, (c0 + e) * p.final_states_stride[1] + i * p.final_states_stride[2], f[e]);
         }
     }
 }
@@ -359,10 +378,8 @@ __global__ void __launch_bounds__(256) fwd_generic(const FwdArgs a) {
 
 namespace {
 
-// channel-last launch shape: channels per lane, steps per tile, steps in flight
-constexpr int kColsCPL = 4;
-constexpr int64_t kColsChunk = 64;
-constexpr int kColsU = 8;
+// channel-last launch shape: time steps per wavefront tile
+constexpr int kClTS = 16;
 
 template <typename T>
 bool rows_vec_ok(const cc1d_fwd_params& p) {
@@ -381,15 +398,20 @@ bool rows_vec_ok(const cc1d_fwd_params& p) {
     return true;
 }
 
-// channel-last with CPL-channel lanes: unit channel stride, CPL | dim and
-// every row start aligned to CPL elements
+// channel-last tiles: unit channel stride, CPL | dim, rows aligned to the
+// CPL-channel lane vector, 32-bit positions inside a batch
 template <typename T, int CPL>
-bool cols_vec_ok(const cc1d_fwd_params& p) {
+bool cl_ok(const cc1d_fwd_params& p) {
     constexpr int64_t NB = CPL * (int64_t)sizeof(T);
     if (p.x_stride[1] != 1 || p.out_stride[1] != 1) return false;
     if (p.dim % CPL != 0) return false;
     if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.out)) % NB) return false;
     if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.out_stride[0] % CPL || p.out_stride[2] % CPL) return false;
+    const int64_t span = p.seqlen + kClTS + 16;  // furthest row a tile touches
+    const int64_t lim = (int64_t)1 << 31;
+    if (p.dim >= lim || span * p.x_stride[2] >= lim || span * p.out_stride[2] >= lim) return false;
+    if (p.seq_idx != nullptr && span * p.seq_idx_stride[1] >= lim) return false;
+    if (p.batch * ceil_div(p.dim / CPL, 64) * ceil_div(p.seqlen, kClTS) >= lim * 2) return false;
     return true;
 }
 
@@ -425,16 +447,16 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         });
                     }
                 }
-                constexpr int CPL = kColsCPL;
-                if (cols_vec_ok<T, CPL>(p)) {
+                constexpr int CPL = 4 / (int)sizeof(T);
+                if (cl_ok<T, CPL>(p)) {
                     a.ngroups = ceil_div(p.dim / CPL, 64);
-                    a.chunk = kColsChunk;
-                    a.nseg = ceil_div(p.seqlen, a.chunk);
+                    a.chunk = kClTS;
+                    a.nseg = ceil_div(p.seqlen, kClTS);
                     a.n_items = p.batch * a.nseg * a.ngroups;
                     const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                     return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                         constexpr bool SEQ = decltype(qc)::value;
-                        fwd_cols_vec<T, W, CPL, kColsU, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
+                        fwd_cl<T, W, CPL, kClTS, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
                         return launch_status();
                     });
                 }

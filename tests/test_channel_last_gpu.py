@@ -1,0 +1,148 @@
+"""Channel-last inputs (x viewed from a (batch, seqlen, dim) buffer, unit
+channel stride) on MI355X vs the oracle, forward and backward.
+
+The reference runs this layout through its strided path
+(tests/test_noncontig_layouts.py); here it has its own tiled kernels, so the
+tile edges get their own cases: sequence lengths around the 16-step tile,
+shorter than the halo, dims that leave a partial channel group, odd dims (the
+generic fallback), seq_idx patterns whose boundaries fall inside tiles
+(including ids that reappear within one window), padding, initial and final
+states with their gradients, and widths 2..9.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import causal_conv1d_amd as cc
+from _util import (
+    DTYPE_IDS,
+    DTYPES,
+    SEQ_PATTERNS,
+    assert_close,
+    assert_equal,
+    assert_reduction_close,
+    make_inputs,
+    seq_pattern,
+)
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _cl(t):
+    """(B, D, L) values in a channel-last buffer on the GPU: strides (L*D, 1, D)."""
+    return t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+
+
+def _widths(dtype):
+    return [2, 3, 4, 5] if dtype == torch.float32 else [2, 3, 4, 5, 9]
+
+
+def _fwd_cases():
+    for dtype, did in zip(DTYPES, DTYPE_IDS):
+        for width in _widths(dtype):
+            yield pytest.param(dtype, width, id=f"{did}-w{width}")
+
+
+@pytest.mark.parametrize("dtype,width", list(_fwd_cases()))
+@pytest.mark.parametrize("seqlen", [1, 3, 16, 17, 100, 515])
+@pytest.mark.parametrize("dim", [64, 130, 33])
+def test_cl_forward(dtype, width, seqlen, dim):
+    x, w, b, _ = make_inputs(2, dim, seqlen, width, dtype=dtype)
+    xg = _cl(x)
+    assert xg.stride(1) == 1
+    gpu = cc.causal_conv1d_fn(xg, w.to(DEV), b.to(DEV), activation="silu").cpu()
+    assert_close(gpu, O.causal_conv1d_fn(x, w, b, activation="silu"), dtype)
+
+
+@pytest.mark.parametrize("pattern", SEQ_PATTERNS)
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 4, 5])
+@pytest.mark.parametrize("seqlen", [40, 515])
+def test_cl_forward_seq_idx(pattern, dtype, width, seqlen):
+    x, w, b, _ = make_inputs(2, 130, seqlen, width, dtype=dtype)
+    s = seq_pattern(pattern, 2, seqlen)
+    gpu = cc.causal_conv1d_fn(_cl(x), w.to(DEV), b.to(DEV), seq_idx=s.to(DEV), activation="silu").cpu()
+    assert_close(gpu, O.causal_conv1d_fn(x, w, b, seq_idx=s, activation="silu"), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 4, 5])
+@pytest.mark.parametrize("seqlen", [1, 2, 3, 20, 100])
+def test_cl_forward_states(dtype, width, seqlen):
+    x, w, b, init = make_inputs(2, 64, seqlen, width, dtype=dtype, has_init=True)
+    out, fs = cc.causal_conv1d_fn(_cl(x), w.to(DEV), b.to(DEV), initial_states=init.to(DEV),
+                                  return_final_states=True, activation="silu")
+    rout, rfs = O.causal_conv1d_fn(x, w, b, initial_states=init, return_final_states=True, activation="silu")
+    assert_close(out.cpu(), rout, dtype)
+    assert_equal(fs.cpu(), rfs, name="final_states")
+
+
+def _grads(x, w, b, dout, *, init=None, seq_idx=None, dfs=None):
+    """Autograd through a channel-last view; gradients come back as (B, D, L) values."""
+    base = x.transpose(1, 2).contiguous().to(DEV).requires_grad_()
+    wg = w.to(DEV).requires_grad_()
+    bg = b.to(DEV).requires_grad_()
+    ig = init.to(DEV).requires_grad_() if init is not None else None
+    kw = dict(initial_states=ig, activation="silu", seq_idx=None if seq_idx is None else seq_idx.to(DEV))
+    if dfs is not None:
+        out, fs = cc.causal_conv1d_fn(base.transpose(1, 2), wg, bg, return_final_states=True, **kw)
+        torch.autograd.backward([out, fs], [dout.to(DEV), dfs.to(DEV)])
+    else:
+        cc.causal_conv1d_fn(base.transpose(1, 2), wg, bg, **kw).backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    return (base.grad.transpose(1, 2).cpu(), wg.grad.cpu(), bg.grad.cpu(),
+            None if ig is None else ig.grad.cpu())
+
+
+def _check(got, ref, dtype, has_init=False):
+    dx, dw, db, di = got
+    rdx, rdw, rdb, rdi = ref
+    assert_close(dx, rdx, dtype, name="dx")
+    assert_reduction_close(dw, rdw, dtype, name="dweight")
+    assert_reduction_close(db, rdb, dtype, name="dbias")
+    if has_init:
+        assert_close(di, rdi, dtype, name="dinitial_states")
+
+
+@pytest.mark.parametrize("dtype,width", list(_fwd_cases()))
+@pytest.mark.parametrize("seqlen", [1, 3, 16, 17, 100, 515])
+@pytest.mark.parametrize("dim", [64, 130, 33])
+def test_cl_backward(dtype, width, seqlen, dim):
+    x, w, b, _ = make_inputs(2, dim, seqlen, width, dtype=dtype)
+    dout = make_inputs(2, dim, seqlen, width, dtype=dtype, seed=1)[0]
+    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype)
+
+
+@pytest.mark.parametrize("pattern", SEQ_PATTERNS)
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 4, 5])
+@pytest.mark.parametrize("seqlen", [40, 515])
+def test_cl_backward_seq_idx(pattern, dtype, width, seqlen):
+    x, w, b, _ = make_inputs(2, 130, seqlen, width, dtype=dtype)
+    dout = make_inputs(2, 130, seqlen, width, dtype=dtype, seed=1)[0]
+    s = seq_pattern(pattern, 2, seqlen)
+    _check(_grads(x, w, b, dout, seq_idx=s), O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 4, 5])
+@pytest.mark.parametrize("seqlen", [1, 2, 3, 20, 100])
+def test_cl_backward_states(dtype, width, seqlen):
+    x, w, b, init = make_inputs(2, 64, seqlen, width, dtype=dtype, has_init=True)
+    dout = make_inputs(2, 64, seqlen, width, dtype=dtype, seed=1)[0]
+    dfs = make_inputs(2, 64, width - 1, width, dtype=dtype, seed=2)[0]
+    got = _grads(x, w, b, dout, init=init, dfs=dfs)
+    ref = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init, dfinal_states=dfs, activation="silu")
+    _check(got, ref, dtype, has_init=True)
+
+
+def test_cl_backward_many_tile_groups():
+    """Several blocks of tiles per row and several batches: the LDS block reduction feeds each
+    channel's accumulators from many blocks."""
+    x, w, b, _ = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16)
+    dout = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16, seed=1)[0]
+    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), torch.bfloat16)
