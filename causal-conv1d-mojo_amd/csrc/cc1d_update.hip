@@ -15,8 +15,11 @@
 //                     out and contiguous state rows: a lane owns EPV adjacent
 //                     channels of 2 batch entries, so x, out, weight and the
 //                     (EPV x S) state blocks move as 16-byte vectors.
-//   update_circ    -- circular mode with up to 8 new tokens; one thread per
-//                     (b, c) with all loads issued before any store.
+//   update_circ_vec -- circular mode on contiguous state lines of whole
+//                     16-byte chunks: one thread per (b, c) reads and writes
+//                     the one or two chunks that hold its window.
+//   update_circ    -- other circular cases with up to 8 new tokens; one thread
+//                     per (b, c) with all loads issued before any store.
 //   update_generic -- everything else; one thread per (b, c).
 // Both use the forward's tap loop (fma in k order, then SiLU), so a decode
 // loop reproduces the full forward bit for bit.
@@ -248,6 +251,148 @@ __global__ void __launch_bounds__(256) update_circ(const UpdArgs a) {
     }
 }
 
+// Replace element e (compile-time after unrolling) of a 16-byte vector by
+// the raw bits of a T.
+template <typename T> __device__ __forceinline__ void vset_raw(u32x4& v, int e, uint32_t bits) {
+    if constexpr (sizeof(T) == 4) {
+        v[e] = bits;
+    } else {
+        const uint32_t d = v[e >> 1];
+        v[e >> 1] = (e & 1) ? ((d & 0x0000ffffu) | (bits << 16)) : ((d & 0xffff0000u) | (bits & 0xffffu));
+    }
+}
+template <typename T> __device__ __forceinline__ uint32_t raw_bits(const T* p) {
+    if constexpr (sizeof(T) == 4) return *reinterpret_cast<const uint32_t*>(p);
+    else return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Circular mode on contiguous, 16-byte aligned state lines whose length is a
+// multiple of the 16-byte chunk (EPV elements), with a window of W-1 history
+// plus Ls new positions that spans at most two chunks. One thread per (b, c),
+// lanes on adjacent channels. The window starts at offset O (compile-time)
+// inside its first chunk, so every element access is a register access; the
+// thread reads the one or two chunks of its window as 16-byte vectors, writes
+// the new tokens into them and stores them back whole (the other positions
+// of a chunk are written back unchanged; only this thread touches this state
+// line).
+template <typename T, int W, bool SILU, bool DW, int O>
+__device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, uint32_t b, uint32_t c, T* sl,
+                                                   int32_t ka, int32_t kb, int Ls, const uint32_t* xb,
+                                                   const float* w, float bias) {
+    constexpr int H = W - 1;
+    constexpr int EPV = elems16<T>::value;
+    constexpr int LMAX = EPV + 1 - H;  // most new tokens a two-chunk window holds
+    const bool cross = O + H + Ls > EPV;
+    u32x4 va = vload(sl + ka * EPV);
+    u32x4 vb = vload(sl + kb * EPV);  // unconditional: the loads issue together
+
+    float win[W];
+#pragma unroll
+    for (int i = 0; i < H; ++i) win[i] = (O + i < EPV) ? vget<T>(va, O + i) : vget<T>(vb, O + i - EPV);
+    T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+    float o[LMAX];
+#pragma unroll
+    for (int i = 0; i < LMAX; ++i) {
+        o[i] = 0.0f;
+        if (i < Ls) {
+            const int q = O + H + i;  // window position of new token i
+            if (q < EPV) vset_raw<T>(va, q, xb[i]);
+            else vset_raw<T>(vb, q - EPV, xb[i]);
+            u32x4 one = vzero();
+            vset_raw<T>(one, 0, xb[i]);
+            win[H] = vget<T>(one, 0);
+            float acc = conv_taps<W>(bias, w, win);
+            if constexpr (SILU) acc = silu(acc);
+            o[i] = acc;
+            if constexpr (!DW) st(orow, i * p.out_stride[2], acc);
+#pragma unroll
+            for (int k = 0; k < H; ++k) win[k] = win[k + 1];
+        }
+    }
+    if constexpr (DW) {  // the Ls outputs as whole dwords
+        constexpr int PER = 4 / (int)sizeof(T);
+#pragma unroll
+        for (int d = 0; d < (LMAX + PER - 1) / PER; ++d) {
+            if (d * PER < Ls) {
+                uint32_t v;
+                if constexpr (PER == 1) v = __float_as_uint(o[d]);
+                else v = (uint32_t)from_f32<T>(o[2 * d]).bits | ((uint32_t)from_f32<T>(o[2 * d + 1 < LMAX ? 2 * d + 1 : 0]).bits << 16);
+                reinterpret_cast<uint32_t*>(orow)[d] = v;
+            }
+        }
+    }
+    vstore(sl + ka * EPV, va);
+    if (cross) vstore(sl + kb * EPV, vb);
+}
+
+template <typename T, int W, bool SILU, bool DW>
+__global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
+    constexpr int H = W - 1;
+    constexpr int EPV = elems16<T>::value;
+    constexpr int LMAX = EPV + 1 - H;
+    static_assert(LMAX >= 1, "window must fit in two chunks");
+    const cc1d_update_params& p = a.p;
+    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint32_t)a.n_items) return;
+    const uint32_t D = (uint32_t)p.dim;
+    const uint32_t b = idx / D;
+    const uint32_t c = idx - b * D;
+    const int Ls = (int)p.seqlen;
+    // inputs that do not depend on the state row first, so their loads overlap
+    // the index / cache_seqlens reads the state addresses wait for
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
+    uint32_t xb[LMAX];
+    if constexpr (DW) {  // the Ls tokens as whole dwords
+        constexpr int PER = 4 / (int)sizeof(T);
+#pragma unroll
+        for (int d = 0; d < (LMAX + PER - 1) / PER; ++d) {
+            const uint32_t v = d * PER < Ls ? reinterpret_cast<const uint32_t*>(xr)[d] : 0u;
+#pragma unroll
+            for (int e = 0; e < PER; ++e)
+                if (d * PER + e < LMAX) xb[d * PER + e] = PER == 1 ? v : ((v >> (16 * e)) & 0xffffu);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < LMAX; ++i) xb[i] = i < Ls ? raw_bits(xr + i * p.x_stride[2]) : 0u;
+    }
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k)
+        w[k] = ld(static_cast<const T*>(p.weight), (int64_t)c * p.weight_stride[0] + k * p.weight_stride[1]);
+    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), (int64_t)c * p.bias_stride) : 0.0f;
+
+    const int64_t row = state_row(p, b);
+    if (row < 0) {
+        T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+        for (int i = 0; i < Ls; ++i) st(orow, i * p.out_stride[2], 0.0f);
+        return;
+    }
+    const int32_t S = (int32_t)p.state_len;
+    T* __restrict__ sl = static_cast<T*>(p.conv_state) + row * p.conv_state_stride[0] + c * p.conv_state_stride[1];
+    int32_t cs = p.cache_seqlens[b] % S;
+    if (cs < 0) cs += S;  // floored modulo (torch.remainder)
+    int32_t p0 = cs - H;  // first window position
+    if (p0 < 0) p0 += S;
+    const int32_t ka = p0 / EPV;
+    const int32_t kb = ka + 1 < S / EPV ? ka + 1 : 0;  // the chunk after ka, cyclically
+    switch (p0 % EPV) {
+        case 0: update_circ_chunks<T, W, SILU, DW, 0>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+        case 1: update_circ_chunks<T, W, SILU, DW, 1>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+        case 2: update_circ_chunks<T, W, SILU, DW, 2>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+        case 3: update_circ_chunks<T, W, SILU, DW, 3>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+        default:
+            if constexpr (EPV == 8) {
+                switch (p0 % EPV) {
+                    case 4: update_circ_chunks<T, W, SILU, DW, 4>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+                    case 5: update_circ_chunks<T, W, SILU, DW, 5>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+                    case 6: update_circ_chunks<T, W, SILU, DW, 6>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+                    default: update_circ_chunks<T, W, SILU, DW, 7>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+                }
+            }
+            break;
+    }
+}
+
 namespace {
 
 template <typename T>
@@ -265,6 +410,30 @@ bool vec1_ok(const cc1d_update_params& p) {
     // 32-bit lane indices; size_t offsets
     if (p.batch * p.dim >= ((int64_t)1 << 31) || p.state_rows >= ((int64_t)1 << 31)) return false;
     return true;
+}
+
+// chunked circular mode: contiguous 16-byte aligned state lines of at least
+// two whole chunks, a window of W-1 + seqlen positions within two chunks
+template <typename T>
+bool circ_vec_ok(const cc1d_update_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    if (p.cache_seqlens == nullptr || p.seqlen < 1) return false;
+    if (p.width - 1 + p.seqlen > EPV + 1) return false;
+    // two distinct chunks per line, so a window never wraps onto itself
+    if (p.state_len % EPV != 0 || p.state_len < 2 * EPV) return false;
+    if (p.conv_state_stride[2] != 1 || p.conv_state_stride[1] % EPV || p.conv_state_stride[0] % EPV) return false;
+    if (!aligned16(p.conv_state)) return false;
+    if (p.batch * p.dim >= ((int64_t)1 << 31) || p.state_len >= ((int64_t)1 << 31)) return false;
+    return true;
+}
+
+// tokens of x and out contiguous, a whole number of dwords, dword-aligned rows
+template <typename T>
+bool circ_dwords_ok(const cc1d_update_params& p) {
+    const int64_t e = (int64_t)sizeof(T);
+    if (p.x_stride[2] != 1 || p.out_stride[2] != 1 || (p.seqlen * e) % 4) return false;
+    if (((p.x_stride[0] | p.x_stride[1] | p.out_stride[0] | p.out_stride[1]) * e) % 4) return false;
+    return ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.out)) & 3u) == 0;
 }
 
 }  // namespace
@@ -289,6 +458,14 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                 }
                 a.n_items = p.batch * p.dim;
                 const dim3 grid((unsigned)ceil_div(a.n_items, 256));
+                if constexpr (W - 1 <= EPV) {
+                    if (circ_vec_ok<T>(p)) {
+                        return with_flag(circ_dwords_ok<T>(p), [&](auto dc) {
+                            update_circ_vec<T, W, SILU, decltype(dc)::value><<<grid, 256, 0, stream>>>(a);
+                            return launch_status();
+                        });
+                    }
+                }
                 if (p.cache_seqlens != nullptr && p.seqlen <= 8) {
                     update_circ<T, W, SILU, 8><<<grid, 256, 0, stream>>>(a);
                     return launch_status();

@@ -107,6 +107,35 @@ def test_circular_decode_loop(dtype):
     assert_equal(torch.cat(dec, -1).cpu(), full.cpu())
 
 
+def _chunk_cases():
+    """Circular updates on state lines of whole 16-byte chunks (the chunked kernel): every
+    window offset inside a chunk, windows that cross a chunk or wrap past the line end."""
+    for dtype, did in zip(DTYPES, DTYPE_IDS):
+        epv = 16 // torch.tensor([], dtype=dtype).element_size()
+        for width in ([2, 4, 5] if dtype == torch.float32 else [2, 4, 5, 9]):
+            for seqlen in sorted({1, 2, epv + 1 - (width - 1)} - {0}):
+                if seqlen < 1 or width - 1 + seqlen > epv + 1:
+                    continue
+                for S in (2 * epv, 3 * epv, 64):
+                    yield pytest.param(dtype, width, seqlen, S, id=f"{did}-w{width}-L{seqlen}-S{S}")
+
+
+@pytest.mark.parametrize("dtype,width,seqlen,S", list(_chunk_cases()))
+def test_circular_chunked_lines(dtype, width, seqlen, S):
+    B, D = S + 4, 48
+    x, w, b, _ = make_inputs(B, D, seqlen, width, dtype=dtype)
+    pool = make_inputs(B + 3, D, S, width, dtype=dtype, seed=1)[0]
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randperm(B + 3, generator=g)[:B].to(torch.int32)
+    idx[5] = -1  # one padding entry
+    # every head position of the line (plus >= S and negative heads), so every offset in a chunk
+    cs = torch.cat([torch.arange(S), torch.tensor([S, 2 * S + 1, -1, -S - 2])]).to(torch.int32)[:B]
+    out, st, rout, rst = _run(x, pool, w, b, activation="silu", cache_seqlens=cs, conv_state_indices=idx)
+    assert_close(out, rout, dtype)
+    assert torch.all(out[5] == 0)
+    assert_equal(st, rst, name="pool")
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("circular", [False, True])
 @pytest.mark.parametrize("dim", [16, 64])
