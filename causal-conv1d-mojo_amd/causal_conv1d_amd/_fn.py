@@ -14,6 +14,11 @@ Differences in *where* work happens (results are the same):
 * the ``dfinal_states`` tail add of the backward (``_fn.py:308-315``) is done
   inside the backward kernel with the same two roundings (dx rounded to the
   dtype, then the sum rounded again).
+* the autograd backward gets dweight / dbias in their dtype from
+  ``_bwd_typed_inplace`` (one kernel writes fp32 partial sums, one kernel adds
+  them per channel in a fixed order and rounds once) instead of zero-filled
+  fp32 accumulators, atomics and two casts; the sums are fp32 as in the
+  reference, and the same inputs give the same bits on every run.
 * ``dout`` keeps its layout when it already matches ``x`` (the kernels read
   any strides); only a mismatching layout is copied once.
 * widths 6..9 with autograd are accepted at any seqlen (the reference needs
@@ -25,7 +30,7 @@ from __future__ import annotations
 import torch
 
 from causal_conv1d_amd._dtype import _DTYPE_CODE
-from causal_conv1d_amd._native import native_bwd, native_fwd
+from causal_conv1d_amd._native import native_bwd, native_bwd_typed, native_fwd
 
 
 def _fwd_inplace_impl(
@@ -105,6 +110,53 @@ _bwd_full_inplace = torch.library.custom_op(
 _bwd_full_inplace.register_fake(_bwd_full_inplace_fake)
 
 
+def _bwd_typed_inplace_impl(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    dout: torch.Tensor,
+    seq_idx: torch.Tensor | None,
+    initial_states: torch.Tensor | None,
+    dfinal_states: torch.Tensor | None,
+    dx: torch.Tensor,
+    dweight: torch.Tensor,
+    dbias: torch.Tensor | None,
+    dinitial_states: torch.Tensor | None,
+    apply_silu: bool,
+) -> None:
+    native_bwd_typed(
+        x, weight, bias, dout, seq_idx, initial_states, dx, dweight, dbias, dinitial_states, apply_silu,
+        dfinal_states,
+    )
+
+
+def _bwd_typed_inplace_fake(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    dout: torch.Tensor,
+    seq_idx: torch.Tensor | None,
+    initial_states: torch.Tensor | None,
+    dfinal_states: torch.Tensor | None,
+    dx: torch.Tensor,
+    dweight: torch.Tensor,
+    dbias: torch.Tensor | None,
+    dinitial_states: torch.Tensor | None,
+    apply_silu: bool,
+) -> None:
+    return None
+
+
+# The autograd backward's op: the same kernel as _bwd_full_inplace, but the
+# weight/bias gradients come back in their dtype from one extra reduction
+# kernel, instead of two zero-fills, fp32 atomics and two casts.
+_bwd_typed_inplace = torch.library.custom_op(
+    "causal_conv1d_amd::_bwd_typed_inplace",
+    mutates_args=("dx", "dweight", "dbias", "dinitial_states"),
+)(_bwd_typed_inplace_impl)
+_bwd_typed_inplace.register_fake(_bwd_typed_inplace_fake)
+
+
 def _match_layout(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     """Return ``t`` with the memory layout of ``like`` (a copy only if needed)."""
     if t.stride() == like.stride():
@@ -149,17 +201,18 @@ class _CausalConv1dFn(torch.autograd.Function):
         D, W = weight.shape
         dout = _match_layout(dout, x)
         dx = torch.empty_like(x)
-        dweight_acc = torch.zeros(D, W, dtype=torch.float32, device=x.device)
-        dbias_acc = torch.zeros(D, dtype=torch.float32, device=x.device) if ctx.has_bias else None
+        # fp32 sums rounded once to the parameter dtype, as the reference's
+        # accumulators + casts (_fn.py:276-292,317-320)
+        dweight = torch.empty(D, W, dtype=weight.dtype, device=x.device)
+        dbias = torch.empty(D, dtype=bias.dtype, device=x.device) if ctx.has_bias else None
         dinitial_states = torch.empty_like(initial_states) if initial_states is not None else None
         if dfinal_states is not None and dfinal_states.dtype != x.dtype:
             dfinal_states = dfinal_states.to(x.dtype)
-        torch.ops.causal_conv1d_amd._bwd_full_inplace(
-            x, weight, bias, dout, seq_idx, initial_states, dx, dweight_acc, dbias_acc,
-            dinitial_states, ctx.apply_silu, dfinal_states,
+        torch.ops.causal_conv1d_amd._bwd_typed_inplace(
+            x, weight, bias, dout, seq_idx, initial_states, dfinal_states, dx, dweight, dbias,
+            dinitial_states, ctx.apply_silu,
         )
-        dbias = dbias_acc.to(bias.dtype) if ctx.has_bias else None
-        return dx, dweight_acc.to(weight.dtype), dbias, None, dinitial_states, None, None
+        return dx, dweight, dbias, None, dinitial_states, None, None
 
 
 def causal_conv1d_fn(

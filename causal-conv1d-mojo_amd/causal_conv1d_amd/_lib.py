@@ -1,7 +1,8 @@
 """ctypes binding of ``libcc1d_amd.so`` (the C ABI in ``include/cc1d.h``).
 
 The structures below mirror ``cc1d_fwd_params`` / ``cc1d_bwd_params`` /
-``cc1d_update_params`` / ``cc1d_varlen_params`` field for field. The library
+``cc1d_bwd_grads`` / ``cc1d_update_params`` / ``cc1d_varlen_params`` field
+for field. The library
 is loaded on first use; a missing or stale build raises instead of falling
 back to anything else.
 """
@@ -13,7 +14,7 @@ import os
 from pathlib import Path
 
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -48,6 +49,13 @@ class BwdParams(ctypes.Structure):
     ]
 
 
+class BwdGrads(ctypes.Structure):
+    _fields_ = [
+        ("dweight", _vp), ("dbias", _vp), ("workspace", _vp),
+        ("dweight_stride", _i64x2), ("dbias_stride", _i64), ("workspace_floats", _i64),
+    ]
+
+
 class UpdateParams(ctypes.Structure):
     _fields_ = [
         ("x", _vp), ("weight", _vp), ("bias", _vp), ("conv_state", _vp), ("conv_state_indices", _vp),
@@ -74,6 +82,8 @@ EXPORTED_SYMBOLS = (
     "cc1d_strerror",
     "cc1d_fwd",
     "cc1d_bwd",
+    "cc1d_bwd_workspace_floats",
+    "cc1d_bwd_typed",
     "cc1d_update",
     "cc1d_varlen_states",
 )
@@ -106,6 +116,10 @@ def load():
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(st), _vp]
+    lib.cc1d_bwd_workspace_floats.restype = ctypes.c_int64
+    lib.cc1d_bwd_workspace_floats.argtypes = [ctypes.POINTER(BwdParams)]
+    lib.cc1d_bwd_typed.restype = ctypes.c_int
+    lib.cc1d_bwd_typed.argtypes = [ctypes.POINTER(BwdParams), ctypes.POINTER(BwdGrads), _vp]
     got = lib.cc1d_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"causal_conv1d_amd: ABI version mismatch (library {got}, bindings {ABI_VERSION})")

@@ -66,14 +66,11 @@ def native_fwd(x, weight, bias, seq_idx, initial_states, out, apply_silu, final_
     _lib.check(lib.cc1d_fwd(ctypes.byref(p), _stream(x)))
 
 
-def native_bwd(x, weight, bias, dout, seq_idx, initial_states, dx, dweight_acc, dbias_acc, dinitial_states,
-               apply_silu, dfinal_states=None) -> None:
-    _require_device(x)
-    lib = _lib.load()
+def _bwd_params(x, weight, bias, dout, seq_idx, initial_states, dx, dinitial_states, apply_silu, dfinal_states):
     p = _lib.BwdParams()
     p.x, p.weight, p.bias, p.dout = x.data_ptr(), weight.data_ptr(), _ptr(bias), dout.data_ptr()
     p.seq_idx, p.initial_states, p.dfinal_states = _ptr(seq_idx), _ptr(initial_states), _ptr(dfinal_states)
-    p.dx, p.dweight_acc, p.dbias_acc = dx.data_ptr(), dweight_acc.data_ptr(), _ptr(dbias_acc)
+    p.dx = dx.data_ptr()
     p.dinitial_states = _ptr(dinitial_states)
     p.batch, p.dim, p.seqlen = x.shape
     p.width = weight.shape[1]
@@ -85,12 +82,40 @@ def native_bwd(x, weight, bias, dout, seq_idx, initial_states, dx, dweight_acc, 
     _set3(p.initial_states_stride, initial_states)
     _set3(p.dfinal_states_stride, dfinal_states)
     _set3(p.dx_stride, dx)
-    _set2(p.dweight_acc_stride, dweight_acc)
-    p.dbias_acc_stride = dbias_acc.stride(0) if dbias_acc is not None else 0
     _set3(p.dinitial_states_stride, dinitial_states)
     p.dtype = _DTYPE_CODE[x.dtype]
     p.apply_silu = int(bool(apply_silu))
+    return p
+
+
+def native_bwd(x, weight, bias, dout, seq_idx, initial_states, dx, dweight_acc, dbias_acc, dinitial_states,
+               apply_silu, dfinal_states=None) -> None:
+    """cc1d_bwd: adds the fp32 weight/bias-gradient sums into dweight_acc / dbias_acc."""
+    _require_device(x)
+    lib = _lib.load()
+    p = _bwd_params(x, weight, bias, dout, seq_idx, initial_states, dx, dinitial_states, apply_silu, dfinal_states)
+    p.dweight_acc, p.dbias_acc = dweight_acc.data_ptr(), _ptr(dbias_acc)
+    _set2(p.dweight_acc_stride, dweight_acc)
+    p.dbias_acc_stride = dbias_acc.stride(0) if dbias_acc is not None else 0
     _lib.check(lib.cc1d_bwd(ctypes.byref(p), _stream(x)))
+
+
+def native_bwd_typed(x, weight, bias, dout, seq_idx, initial_states, dx, dweight, dbias, dinitial_states,
+                     apply_silu, dfinal_states=None) -> None:
+    """cc1d_bwd_typed: writes dweight / dbias in their dtype from a per-call fp32 workspace."""
+    _require_device(x)
+    lib = _lib.load()
+    p = _bwd_params(x, weight, bias, dout, seq_idx, initial_states, dx, dinitial_states, apply_silu, dfinal_states)
+    n = lib.cc1d_bwd_workspace_floats(ctypes.byref(p))
+    if n < 0:
+        _lib.check(lib.cc1d_bwd_typed(ctypes.byref(p), None, _stream(x)))
+    ws = torch.empty(max(n, 1), dtype=torch.float32, device=x.device)
+    g = _lib.BwdGrads()
+    g.dweight, g.dbias, g.workspace = dweight.data_ptr(), _ptr(dbias), ws.data_ptr()
+    _set2(g.dweight_stride, dweight)
+    g.dbias_stride = dbias.stride(0) if dbias is not None else 0
+    g.workspace_floats = ws.numel()
+    _lib.check(lib.cc1d_bwd_typed(ctypes.byref(p), ctypes.byref(g), _stream(x)))
 
 
 def native_update(x, weight, bias, conv_state, conv_state_indices, cache_seqlens, out, apply_silu) -> None:

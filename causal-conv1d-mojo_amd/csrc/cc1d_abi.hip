@@ -35,6 +35,7 @@ const char* cc1d_strerror(int status) {
     case CC1D_ERR_EXCLUSIVE: return "seq_idx is mutually exclusive with initial_states and final_states";
     case CC1D_ERR_STATE_LEN: return "conv_state length must be >= width - 1";
     case CC1D_ERR_LAUNCH: return "kernel launch failed";
+    case CC1D_ERR_WORKSPACE: return "workspace smaller than cc1d_bwd_workspace_floats()";
     default: return "unknown status";
     }
 }
@@ -80,6 +81,42 @@ int cc1d_bwd(const cc1d_bwd_params* p, void* stream) {
         p->dweight_acc == nullptr)
         return CC1D_ERR_NULL_POINTER;
     return launch_bwd(*p, s);
+}
+
+int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* p) {
+    if (p == nullptr || !valid_dtype(p->dtype) || !valid_width(p->width)) return -1;
+    if (p->batch <= 0 || p->dim <= 0 || p->seqlen <= 0) return 0;
+    return bwd_workspace_floats(*p);
+}
+
+int cc1d_bwd_typed(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
+    if (p == nullptr || g == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
+    if (p->seq_idx != nullptr && (p->initial_states != nullptr || p->dfinal_states != nullptr))
+        return CC1D_ERR_EXCLUSIVE;
+    if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p->dim == 0) return CC1D_OK;
+    if (g->dweight == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (p->batch == 0 || p->seqlen == 0) {
+        // no positions: the gradients are sums over no terms
+        const int64_t ws[3] = {0, g->dweight_stride[0], g->dweight_stride[1]};
+        int st = launch_zero3(g->dweight, esize(p->dtype), 1, p->dim, p->width, ws, s);
+        if (st == CC1D_OK && g->dbias != nullptr) {
+            const int64_t bs[3] = {0, g->dbias_stride, 0};
+            st = launch_zero3(g->dbias, esize(p->dtype), 1, p->dim, 1, bs, s);
+        }
+        if (st == CC1D_OK && p->dinitial_states != nullptr && p->batch > 0)
+            st = launch_zero3(p->dinitial_states, esize(p->dtype), p->batch, p->dim, p->width - 1,
+                              p->dinitial_states_stride, s);
+        return st;
+    }
+    if (!grid_fits(p->batch * p->dim * p->seqlen)) return CC1D_ERR_SHAPE;
+    if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr || g->workspace == nullptr)
+        return CC1D_ERR_NULL_POINTER;
+    return launch_bwd_typed(*p, *g, s);
 }
 
 int cc1d_update(const cc1d_update_params* p, void* stream) {

@@ -25,6 +25,7 @@ namespace cc1d {
 
 struct BwdArgs {
     cc1d_bwd_params p;
+    float* part;      // non-null: write weight/bias-gradient partial sums here instead of atomics
     int64_t nseg;     // rows_vec: segments per row; cl: tile groups per row; generic: chunks per row
     int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
     int64_t chunk;    // cl: time steps per tile; generic: time steps per thread
@@ -353,10 +354,13 @@ __global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
         const float s = wave_sum(pw[k]);
         if (lane == k) mine = s;
     }
-    if (lane < W)
+    if (a.part != nullptr) {  // record (W taps, bias) of this item
+        if (lane <= W) a.part[(int64_t)item * (W + 1) + lane] = mine;
+    } else if (lane < W) {
         unsafeAtomicAdd(p.dweight_acc + (int64_t)c * p.dweight_acc_stride[0] + lane * p.dweight_acc_stride[1], mine);
-    else if (lane == W && p.dbias_acc != nullptr)
+    } else if (lane == W && p.dbias_acc != nullptr) {
         unsafeAtomicAdd(p.dbias_acc + (int64_t)c * p.dbias_acc_stride, mine);
+    }
 }
 
 // One channel c of batch b over steps [t0, t1), any strides: writes dx (and
@@ -696,7 +700,9 @@ __global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
         float sum = 0.0f;
 #pragma unroll
         for (int q = 0; q < WPB; ++q) sum += red[q][idx];
-        if (idx < NC * W) {
+        if (a.part != nullptr) {  // the block's record: NC channels x W taps, then NC bias sums
+            a.part[(int64_t)blockIdx.x * NE + idx] = sum;
+        } else if (idx < NC * W) {
             const int32_t c = cw0 + idx / W;
             if (c < (int32_t)p.dim)
                 unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + (idx % W) * p.dweight_acc_stride[1], sum);
@@ -722,6 +728,12 @@ __global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
     float pw[W], pb;
     bwd_chunk<T, W, SILU>(p, b, c, t0, t1, pw, pb);
     (void)H;
+    if (a.part != nullptr) {  // record (W taps, bias) of this thread's chunk
+#pragma unroll
+        for (int k = 0; k < W; ++k) a.part[idx * (W + 1) + k] = pw[k];
+        a.part[idx * (W + 1) + W] = pb;
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < W; ++k)
         unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], pw[k]);
@@ -771,55 +783,205 @@ bool cl_ok(const cc1d_bwd_params& p) {
     return true;
 }
 
+
+// ---- launch planning ----------------------------------------------------
+
+enum BwdKind { kBwdRows = 0, kBwdCl = 1, kBwdGeneric = 2 };
+
+// Kernel choice and launch geometry for one call; shared by the launch, the
+// workspace size and the partial-sum reduction.
+struct BwdPlan {
+    int kind;
+    int vpt;           // rows: 16-byte vectors per lane
+    int cpl;           // cl: channels per lane
+    BwdArgs a;
+    int64_t blocks;
+    int64_t records;   // partial-sum records (rows / generic: items; cl: blocks)
+    int64_t rec_floats;
+};
+
+template <typename T, int W>
+BwdPlan plan_bwd(const cc1d_bwd_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    BwdPlan pl;
+    pl.a.p = p;
+    pl.a.part = nullptr;
+    pl.a.chunk = 0;
+    pl.a.groups = 0;
+    pl.vpt = 0;
+    pl.cpl = 0;
+    pl.rec_floats = W + 1;
+    if (W - 1 <= EPV && rows_vec_ok<T>(p)) {
+        const int64_t nvec = p.seqlen / EPV;
+        const int64_t per = ceil_div(nvec, 64);
+        pl.kind = kBwdRows;
+        pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+        pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
+        pl.a.n_items = p.batch * p.dim * pl.a.nseg;
+        pl.blocks = pl.a.n_items;
+        pl.records = pl.a.n_items;
+        return pl;
+    }
+    constexpr int CPL = 4 / (int)sizeof(T);
+    if (cl_ok<T, CPL>(p)) {
+        pl.kind = kBwdCl;
+        pl.cpl = CPL;
+        pl.a.groups = ceil_div(p.dim / CPL, 64);
+        pl.a.chunk = kClTS;
+        pl.a.nseg = ceil_div(ceil_div(p.seqlen, kClTS), kClWPB);  // tile groups per row
+        pl.a.n_items = 0;
+        pl.blocks = p.batch * pl.a.groups * pl.a.nseg;
+        pl.records = pl.blocks;
+        pl.rec_floats = 64 * CPL * (W + 1);
+        return pl;
+    }
+    pl.kind = kBwdGeneric;
+    pl.a.chunk = 64;
+    pl.a.nseg = ceil_div(p.seqlen, pl.a.chunk);
+    pl.a.n_items = p.batch * p.dim * pl.a.nseg;
+    pl.blocks = ceil_div(pl.a.n_items, 256);
+    pl.records = pl.a.n_items;
+    return pl;
+}
+
+template <typename T, int W, bool SILU>
+int launch_plan(BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream) {
+    const dim3 grid((unsigned)pl.blocks);
+    BwdArgs& a = pl.a;
+    if (pl.kind == kBwdRows) {
+        if constexpr (W - 1 <= elems16<T>::value) {
+            return with_flag(p.seq_idx != nullptr, [&](auto qc) {
+                constexpr bool SEQ = decltype(qc)::value;
+                if (pl.vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                else if (pl.vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                return launch_status();
+            });
+        }
+        return CC1D_ERR_SHAPE;  // not reached: the plan only picks rows when the halo fits
+    }
+    if (pl.kind == kBwdCl) {
+        constexpr int CPL = 4 / (int)sizeof(T);
+        return with_flag(p.seq_idx != nullptr, [&](auto qc) {
+            constexpr bool SEQ = decltype(qc)::value;
+            bwd_cl<T, W, CPL, kClTS, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
+            return launch_status();
+        });
+    }
+    bwd_generic<T, W, SILU><<<grid, 256, 0, stream>>>(a);
+    return launch_status();
+}
+
+// Sum of the partial records of each channel, in a fixed order, written in
+// the dtype: one block per 64 channels; the 16 wavefronts of a block take
+// every 16th record of the channel and are summed through LDS.
+struct RedArgs {
+    const float* part;
+    void* dweight;
+    void* dbias;
+    int64_t dweight_stride[2];
+    int64_t dbias_stride;
+    int64_t batch, dim, nseg, groups;
+    int kind;
+    int nc;  // cl: channels per record
+};
+
+template <typename T, int W>
+__global__ void __launch_bounds__(1024) bwd_reduce(const RedArgs r) {
+    constexpr int SPLIT = 16;
+    __shared__ float acc[SPLIT][W + 1][64];
+    const int ci = threadIdx.x & 63;
+    const int sp = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * 64 + ci;
+    float s[W + 1];
+#pragma unroll
+    for (int k = 0; k <= W; ++k) s[k] = 0.0f;
+    if (c < r.dim) {
+        const int64_t n = r.batch * r.nseg;  // records per channel
+        for (int64_t j = sp; j < n; j += SPLIT) {
+            const int64_t b = j / r.nseg, q = j - b * r.nseg;
+            if (r.kind == kBwdCl) {
+                const int64_t g = c / r.nc, cc = c - g * r.nc;
+                const float* rec = r.part + ((b * r.nseg + q) * r.groups + g) * (int64_t)r.nc * (W + 1);
+#pragma unroll
+                for (int k = 0; k < W; ++k) s[k] += rec[cc * W + k];
+                s[W] += rec[(int64_t)r.nc * W + cc];
+            } else {
+                const int64_t item = r.kind == kBwdRows ? (b * r.dim + c) * r.nseg + q : (b * r.nseg + q) * r.dim + c;
+                const float* rec = r.part + item * (W + 1);
+#pragma unroll
+                for (int k = 0; k <= W; ++k) s[k] += rec[k];
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k <= W; ++k) acc[sp][k][ci] = s[k];
+    __syncthreads();
+    if (sp == 0 && c < r.dim) {
+#pragma unroll
+        for (int k = 0; k <= W; ++k) {
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < SPLIT; ++q) t += acc[q][k][ci];
+            if (k < W) st(static_cast<T*>(r.dweight), c * r.dweight_stride[0] + k * r.dweight_stride[1], t);
+            else if (r.dbias != nullptr) st(static_cast<T*>(r.dbias), c * r.dbias_stride, t);
+        }
+    }
+}
+
 }  // namespace
 
 int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
     return with_dtype(p.dtype, [&](auto tag) {
         using T = decltype(tag);
-        constexpr int64_t EPV = elems16<T>::value;
         return with_width(p.width, [&](auto wc) {
             constexpr int W = decltype(wc)::value;
             return with_flag(p.apply_silu != 0, [&](auto sc) {
-                constexpr bool SILU = decltype(sc)::value;
-                BwdArgs a;
-                a.p = p;
-                a.chunk = 0;
-                a.groups = 0;
-                if constexpr (W - 1 <= EPV) {
-                    if (rows_vec_ok<T>(p)) {
-                        const int64_t nvec = p.seqlen / EPV;
-                        const int64_t per = ceil_div(nvec, 64);
-                        const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
-                        a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
-                        a.n_items = p.batch * p.dim * a.nseg;
-                        const dim3 grid((unsigned)a.n_items);
-                        return with_flag(p.seq_idx != nullptr, [&](auto qc) {
-                            constexpr bool SEQ = decltype(qc)::value;
-                            if (vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
-                            else if (vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
-                            else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
-                            return launch_status();
-                        });
-                    }
-                }
-                constexpr int CPL = 4 / (int)sizeof(T);
-                if (cl_ok<T, CPL>(p)) {
-                    a.groups = ceil_div(p.dim / CPL, 64);
-                    a.chunk = kClTS;
-                    a.nseg = ceil_div(ceil_div(p.seqlen, kClTS), kClWPB);  // tile groups per row
-                    a.n_items = 0;
-                    const dim3 grid((unsigned)(p.batch * a.groups * a.nseg));
-                    return with_flag(p.seq_idx != nullptr, [&](auto qc) {
-                        constexpr bool SEQ = decltype(qc)::value;
-                        bwd_cl<T, W, CPL, kClTS, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
-                        return launch_status();
-                    });
-                }
-                a.chunk = 64;
-                a.nseg = ceil_div(p.seqlen, a.chunk);
-                a.n_items = p.batch * p.dim * a.nseg;
-                const dim3 grid((unsigned)ceil_div(a.n_items, 256));
-                bwd_generic<T, W, SILU><<<grid, 256, 0, stream>>>(a);
+                BwdPlan pl = plan_bwd<T, W>(p);
+                return launch_plan<T, W, decltype(sc)::value>(pl, p, stream);
+            });
+        });
+    });
+}
+
+int64_t bwd_workspace_floats(const cc1d_bwd_params& p) {
+    int64_t n = -1;
+    with_dtype(p.dtype, [&](auto tag) {
+        using T = decltype(tag);
+        return with_width(p.width, [&](auto wc) {
+            const BwdPlan pl = plan_bwd<T, decltype(wc)::value>(p);
+            n = pl.records * pl.rec_floats;
+            return (int)CC1D_OK;
+        });
+    });
+    return n;
+}
+
+int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream) {
+    return with_dtype(p.dtype, [&](auto tag) {
+        using T = decltype(tag);
+        return with_width(p.width, [&](auto wc) {
+            constexpr int W = decltype(wc)::value;
+            return with_flag(p.apply_silu != 0, [&](auto sc) {
+                BwdPlan pl = plan_bwd<T, W>(p);
+                if (pl.records * pl.rec_floats > g.workspace_floats) return (int)CC1D_ERR_WORKSPACE;
+                pl.a.part = g.workspace;
+                const int st = launch_plan<T, W, decltype(sc)::value>(pl, p, stream);
+                if (st != CC1D_OK) return st;
+                RedArgs r;
+                r.part = g.workspace;
+                r.dweight = g.dweight;
+                r.dbias = g.dbias;
+                r.dweight_stride[0] = g.dweight_stride[0];
+                r.dweight_stride[1] = g.dweight_stride[1];
+                r.dbias_stride = g.dbias_stride;
+                r.batch = p.batch;
+                r.dim = p.dim;
+                r.nseg = pl.a.nseg;
+                r.groups = pl.a.groups;
+                r.kind = pl.kind;
+                r.nc = 64 * (pl.cpl > 0 ? pl.cpl : 1);
+                bwd_reduce<T, W><<<dim3((unsigned)ceil_div(p.dim, 64)), 1024, 0, stream>>>(r);
                 return launch_status();
             });
         });

@@ -14,6 +14,8 @@ namespace cc1d {
 // ABI layer; each returns a cc1d_status.
 int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream);
 int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream);
+int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream);
+int64_t bwd_workspace_floats(const cc1d_bwd_params& p);
 int launch_update(const cc1d_update_params& p, hipStream_t stream);
 int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream);
 

@@ -26,6 +26,8 @@
  *                         fed by native_fwd's 29-int tuple, src/causal_conv1d_mojo/fwd/__init__.py:11-60
  *   cc1d_bwd           <- causal_conv1d_bwd_full_variant, src/causal_conv1d_mojo/bwd_full/variant.mojo:50-144,
  *                         fed by native_bwd_full, src/causal_conv1d_mojo/bwd_full/__init__.py:11-73
+ *   cc1d_bwd_typed     <- the same kernel plus the accumulator zero-fill and the casts of the
+ *                         autograd backward, src/causal_conv1d_mojo/_fn.py:276-292,317-320
  *   cc1d_update        <- causal_conv1d_update_variant, src/causal_conv1d_mojo/update/variant.mojo:45-116,
  *                         fed by native_update, src/causal_conv1d_mojo/update/__init__.py:11-60
  *   cc1d_varlen_states <- causal_conv1d_varlen_states (pure torch in the reference),
@@ -40,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CC1D_ABI_VERSION 1
+#define CC1D_ABI_VERSION 2
 
 enum cc1d_dtype {
     CC1D_DTYPE_FP16 = 0,
@@ -56,7 +58,8 @@ enum cc1d_status {
     CC1D_ERR_SHAPE = 4,             /* negative size, or a size/stride too large for the kernels */
     CC1D_ERR_EXCLUSIVE = 5,         /* seq_idx given together with initial_states or final_states */
     CC1D_ERR_STATE_LEN = 6,         /* conv_state length < width - 1 */
-    CC1D_ERR_LAUNCH = 7             /* the HIP runtime refused a kernel launch */
+    CC1D_ERR_LAUNCH = 7,            /* the HIP runtime refused a kernel launch */
+    CC1D_ERR_WORKSPACE = 8          /* workspace smaller than cc1d_bwd_workspace_floats() */
 };
 
 /*
@@ -128,6 +131,22 @@ typedef struct cc1d_bwd_params {
 } cc1d_bwd_params;
 
 /*
+ * Weight/bias gradients in the dtype for cc1d_bwd_typed. The backward kernel
+ * writes fp32 partial sums to `workspace` (no atomics, nothing to zero
+ * first); a second kernel sums each channel's partials in a fixed order and
+ * writes dweight (and dbias) rounded once to the dtype, so the result is the
+ * same on every run.
+ */
+typedef struct cc1d_bwd_grads {
+    void* dweight;                 /* (dim, width), dtype of the call */
+    void* dbias;                   /* (dim,) or NULL */
+    float* workspace;              /* at least cc1d_bwd_workspace_floats() floats */
+    int64_t dweight_stride[2];
+    int64_t dbias_stride;
+    int64_t workspace_floats;      /* capacity of workspace */
+} cc1d_bwd_grads;
+
+/*
  * Decode update. x holds `seqlen` new tokens per (batch, channel). Linear
  * mode (cache_seqlens == NULL): the state row becomes the last state_len
  * values of cat(state, x). Circular mode: x[i] is written at
@@ -179,6 +198,18 @@ const char* cc1d_strerror(int status);
 
 int cc1d_fwd(const cc1d_fwd_params* params, void* stream);
 int cc1d_bwd(const cc1d_bwd_params* params, void* stream);
+
+/*
+ * Backward with typed weight/bias gradients (what causal_conv1d_fn's
+ * autograd backward returns, src/causal_conv1d_mojo/_fn.py:258-332): dx,
+ * dinitial_states and the dfinal_states tail as in cc1d_bwd, and
+ * dweight/dbias written through `grads` instead of accumulated into
+ * params->dweight_acc / dbias_acc (ignored here). Two kernels; no fill.
+ * cc1d_bwd_workspace_floats returns the workspace size for these params
+ * (< 0 for an invalid dtype or width).
+ */
+int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* params);
+int cc1d_bwd_typed(const cc1d_bwd_params* params, const cc1d_bwd_grads* grads, void* stream);
 int cc1d_update(const cc1d_update_params* params, void* stream);
 int cc1d_varlen_states(const cc1d_varlen_params* params, void* stream);
 

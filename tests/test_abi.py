@@ -33,7 +33,7 @@ def lib():
 
 def _declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cc1d_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(cc1d_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_the_bound_entry_points():
@@ -50,8 +50,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.cc1d_abi_version() == _lib.ABI_VERSION == 1
-    for code in range(0, 8):
+    assert lib.cc1d_abi_version() == _lib.ABI_VERSION == 2
+    for code in range(0, 9):
         msg = lib.cc1d_strerror(code).decode()
         assert msg and msg != "unknown status"
     assert lib.cc1d_strerror(99).decode() == "unknown status"
@@ -60,6 +60,7 @@ def test_abi_version_and_strerror(lib):
 STRUCTS = {
     "cc1d_fwd_params": _lib.FwdParams,
     "cc1d_bwd_params": _lib.BwdParams,
+    "cc1d_bwd_grads": _lib.BwdGrads,
     "cc1d_update_params": _lib.UpdateParams,
     "cc1d_varlen_params": _lib.VarlenParams,
 }
@@ -126,6 +127,36 @@ def test_bwd_validation_codes(lib):
     assert call() == ERR_NULL
     assert call(batch=0) == OK
     assert call(seqlen=0) == OK
+
+
+def test_bwd_typed_validation_codes(lib):
+    def params(**kw):
+        p = _lib.BwdParams()
+        p.batch, p.dim, p.seqlen, p.width, p.dtype = 1, 8, 16, 4, 1
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+    def call(grads=True, gkw=None, **kw):
+        g = _lib.BwdGrads()
+        for k, v in (gkw or {}).items():
+            setattr(g, k, v)
+        return lib.cc1d_bwd_typed(ctypes.byref(params(**kw)), ctypes.byref(g) if grads else None, None)
+
+    assert lib.cc1d_bwd_typed(None, None, None) == ERR_NULL
+    assert call(grads=False) == ERR_NULL
+    assert call(dtype=-1) == ERR_DTYPE
+    assert call(width=11) == ERR_WIDTH
+    assert call(seq_idx=16, dfinal_states=16) == ERR_EXCL
+    assert call(initial_states=16) == ERR_NULL  # dinitial_states missing
+    assert call() == ERR_NULL  # dweight missing
+    assert call(gkw=dict(dweight=16)) == ERR_NULL  # x, dout, dx, workspace missing
+    assert call(dim=0) == OK
+    # workspace size: -1 for invalid params, 0 when there is nothing to sum, else positive
+    assert lib.cc1d_bwd_workspace_floats(None) == -1
+    assert lib.cc1d_bwd_workspace_floats(ctypes.byref(params(width=11))) == -1
+    assert lib.cc1d_bwd_workspace_floats(ctypes.byref(params(seqlen=0))) == 0
+    assert lib.cc1d_bwd_workspace_floats(ctypes.byref(params())) > 0
 
 
 def test_update_validation_codes(lib):
