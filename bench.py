@@ -24,9 +24,10 @@ Reported (one JSON line):
 Input sets are rotated so that the data touched between two reuses of a
 buffer exceeds the 256 MB Infinity Cache: every launch streams from HBM.
 
-Modes: --mode bench (default), --mode kernels (eager launch loop for
-rocprofv3 --kernel-trace / --pmc), --mode copy (a plain 1 GiB device copy,
-the calibration kernel for FETCH_SIZE / WRITE_SIZE).
+Modes: --mode bench (default), --mode kernels (eager launch loop of the C2
+forward / backward / C4a update, plus the C3 / C5 / C4b launches unless
+--no-configs, for rocprofv3 --kernel-trace / --pmc), --mode copy (a plain
+1 GiB device copy, the calibration kernel for FETCH_SIZE / WRITE_SIZE).
 """
 
 from __future__ import annotations
@@ -240,10 +241,24 @@ def bench_update(torch, cc, launches):
     g = _graph(torch, loop)
     ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
     us = ms * 1e3
+    del g
+
+    # A decode loop reuses one state pool every step: with one buffer set the 21 MB of
+    # a call stay in the 256 MB Infinity Cache between calls. Reported beside the
+    # HBM-streaming figure above, never as it.
+    def warm_loop():
+        x, pool, idx, out = sets[0]
+        for _ in range(launches):
+            lib_update(x.unsqueeze(-1), w, b, pool, idx, None, out.unsqueeze(-1), True)
+
+    g = _graph(torch, warm_loop)
+    us_warm = min(_time_graph(torch, g, 3) for _ in range(3)) / launches * 1e3
+    del g
     res = {"workload": "C4a: x (256,5120,1) bf16, pool (512,5120,3), 256 random rows, W4, bias, SiLU",
            "us_per_call": round(us, 2), "algorithmic_bytes": UPD_BYTES,
            "gbps": round(UPD_BYTES / (us * 1e-6) / 1e9, 1),
-           "frac_of_peak": round(UPD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "buffer_sets": nsets}
+           "frac_of_peak": round(UPD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "buffer_sets": nsets,
+           "us_per_call_cache_resident": round(us_warm, 2)}
     log(f"update: {res}")
     return res
 
@@ -265,10 +280,12 @@ def _entry(ms, nbytes, **extra):
             "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), **extra}
 
 
-def bench_configs(torch, cc, launches):
-    """Kernel throughput at the other BASELINE configurations (reported, not the headline)."""
+def _config_cases(torch, cc):
+    """Launch closures of the other BASELINE configurations: name -> (closures cycling
+    over rotating buffer sets, algorithmic bytes per launch, launches per timing graph
+    divisor, extra report fields)."""
     ops = torch.ops.causal_conv1d_amd
-    res = {}
+    cases = {}
     # C3: stored (1, 8192, 4096) bf16 channel-last, viewed (1, 4096, 8192); W4, SiLU, no bias
     L3, D3 = 8192, 4096
     sets = []
@@ -292,15 +309,14 @@ def bench_configs(torch, cc, launches):
             ("c3a", (seq, None, None), (seq, None), 32768 + D3 * W * 2, 2 * 32768 + D3 * W * 2 + D3 * W * 4),
             ("c3b", (None, init, fs), (None, init), D3 * W * 2 + 2 * 24576, D3 * W * 2 + D3 * W * 4 + 2 * 24576)):
         s_, i_, f_ = kw_f
-        fns = [lambda x=x, o=o: ops._fwd_inplace(x, w3, None, s_, i_, o, True, f_) for x, _, o, _ in sets]
-        res[f"{name}_fwd"] = _entry(_time_launch_set(torch, fns, launches), 2 * n3 + extra_f)
+        fns = [lambda x=x, o=o, s_=s_, i_=i_, f_=f_: ops._fwd_inplace(x, w3, None, s_, i_, o, True, f_)
+               for x, _, o, _ in sets]
+        cases[f"{name}_fwd"] = (fns, 2 * n3 + extra_f, 1, {})
         sb, ib = kw_b
-        fns = [lambda x=x, d=d, dx=dx: ops._bwd_full_inplace(x, w3, None, d, sb, ib, dx, dw3, None,
-                                                             di if ib is not None else None, True)
+        fns = [lambda x=x, d=d, dx=dx, sb=sb, ib=ib: ops._bwd_full_inplace(x, w3, None, d, sb, ib, dx, dw3, None,
+                                                                           di if ib is not None else None, True)
                for x, d, _, dx in sets]
-        res[f"{name}_bwd"] = _entry(_time_launch_set(torch, fns, launches), 3 * n3 + extra_b)
-        log(f"{name}: fwd {res[name + '_fwd']['us_per_launch']} us, bwd {res[name + '_bwd']['us_per_launch']} us")
-    del sets
+        cases[f"{name}_bwd"] = (fns, 3 * n3 + extra_b, 1, {})
     # C5: (8, 2048, 16384), no bias, no activation, bf16 and fp32 at W4 (W2/W3 in the tests)
     B5, D5, L5 = 8, 2048, 16384
     for dt, tag in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
@@ -311,14 +327,10 @@ def bench_configs(torch, cc, launches):
         w5 = torch.randn(D5, W, generator=g, device="cuda").to(dt)
         dw5 = torch.zeros(D5, W, dtype=torch.float32, device="cuda")
         n5 = B5 * D5 * L5 * es
-        nl = max(4, launches // 8)
-        res[f"c5_{tag}_fwd"] = _entry(_time_launch_set(
-            torch, [lambda: ops._fwd_inplace(x, w5, None, None, None, out, False, None)], nl), 2 * n5 + D5 * W * es)
-        res[f"c5_{tag}_bwd"] = _entry(_time_launch_set(
-            torch, [lambda: ops._bwd_full_inplace(x, w5, None, dout, None, None, dx, dw5, None, None, False)], nl),
-            3 * n5 + D5 * W * (es + 4))
-        log(f"c5 {tag}: fwd {res[f'c5_{tag}_fwd']['us_per_launch']} us, bwd {res[f'c5_{tag}_bwd']['us_per_launch']} us")
-        del x, dout, out, dx
+        cases[f"c5_{tag}_fwd"] = ([lambda x=x, w5=w5, out=out: ops._fwd_inplace(x, w5, None, None, None, out, False,
+                                                                                 None)], 2 * n5 + D5 * W * es, 8, {})
+        cases[f"c5_{tag}_bwd"] = ([lambda x=x, w5=w5, dout=dout, dx=dx, dw5=dw5: ops._bwd_full_inplace(
+            x, w5, None, dout, None, None, dx, dw5, None, None, False)], 3 * n5 + D5 * W * (es + 4), 8, {})
     # C4b: x (256, 5120, 4), circular state_len 64 in a pool of 512, cache_seqlens in [0, 64)
     usets = []
     w4 = torch.randn(D, W, generator=g, device="cuda").bfloat16()
@@ -330,11 +342,21 @@ def bench_configs(torch, cc, launches):
         cs = torch.randint(0, 64, (UPD_B,), generator=g, device="cuda", dtype=torch.int32)
         usets.append((x, pool, idx, cs, torch.empty_like(x)))
     fns = [lambda u=u: cc._native.native_update(u[0], w4, b4, u[1], u[2], u[3], u[4], True) for u in usets]
-    ms = _time_launch_set(torch, fns, launches)
     nb = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4
-    res["update_c4b"] = _entry(ms, nb, us_per_call=round(ms * 1e3, 2),
-                               note="14 of 128 bytes of each state row are touched; DRAM bursts bound this")
-    log(f"c4b update: {res['update_c4b']['us_per_launch']} us")
+    cases["update_c4b"] = (fns, nb, 1, {"note": "14 of 128 bytes of each state row are touched; DRAM bursts "
+                                                "bound this"})
+    return cases
+
+
+def bench_configs(torch, cc, launches):
+    """Kernel throughput at the other BASELINE configurations (reported, not the headline)."""
+    res = {}
+    for name, (fns, nbytes, div, extra) in _config_cases(torch, cc).items():
+        ms = _time_launch_set(torch, fns, max(4, launches // div))
+        res[name] = _entry(ms, nbytes, **extra)
+        if name == "update_c4b":
+            res[name]["us_per_call"] = res[name]["us_per_launch"]
+        log(f"{name}: {res[name]['us_per_launch']} us/launch ({res[name]['frac_of_peak']:.3f} of peak)")
     return res
 
 
@@ -390,14 +412,18 @@ def mode_kernels(torch, cc, args):
     dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
     db = torch.zeros(D, dtype=torch.float32, device="cuda")
     usets, uw, ub = _update_sets(torch, 13)
+    cases = {} if args.no_configs else _config_cases(torch, cc)
     for i in range(args.steps):
         x, dout = sets[i % 3]
         torch.ops.causal_conv1d_amd._fwd_inplace(x, w, b, None, None, outs[i % 3], True, None)
         torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dxs[i % 3], dw, db, None, True)
         ux, pool, idx, uo = usets[i % 13]
         cc._native.native_update(ux.unsqueeze(-1), uw, ub, pool, idx, None, uo.unsqueeze(-1), True)
+        for fns, _, _, _ in cases.values():
+            fns[i % len(fns)]()
     torch.cuda.synchronize()
-    log(f"kernels mode: {args.steps} iterations of fwd + bwd + update done")
+    log(f"kernels mode: {args.steps} iterations of fwd + bwd + update" + ("" if args.no_configs else
+        " + the C3 / C5 / C4b launches") + " done")
 
 
 def mode_copy(torch, args):
