@@ -1,11 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the depthwise causal conv1d hot path on one MI355X.
 
-Workload (the config the metric is quoted on):
+Workload (benchmark configuration C2, the one the headline metric is quoted on):
   C2: x (4, 5120, 2048) bf16 channel-first, weight (5120, 4), bias (5120),
       SiLU, dout N(0,1); one step = forward + backward through the public API
-      (causal_conv1d_fn + torch.autograd.grad), captured as one HIP graph per
-      rotating buffer set so that the step time is GPU time.
+      (causal_conv1d_fn + torch.autograd.grad); one HIP graph holds one step per
+      rotating buffer set, so that the step time is GPU time.
 
 Reported (one JSON line):
   value        step throughput in GB/s = algorithmic bytes of the forward and
@@ -281,7 +281,7 @@ def _entry(ms, nbytes, **extra):
 
 
 def _config_cases(torch, cc):
-    """Launch closures of the other BASELINE configurations: name -> (closures cycling
+    """Launch closures of the other benchmark configurations: name -> (closures cycling
     over rotating buffer sets, algorithmic bytes per launch, launches per timing graph
     divisor, extra report fields)."""
     ops = torch.ops.causal_conv1d_amd
@@ -349,7 +349,7 @@ def _config_cases(torch, cc):
 
 
 def bench_configs(torch, cc, launches):
-    """Kernel throughput at the other BASELINE configurations (reported, not the headline)."""
+    """Kernel throughput at the other benchmark configurations (reported, not the headline)."""
     res = {}
     for name, (fns, nbytes, div, extra) in _config_cases(torch, cc).items():
         ms = _time_launch_set(torch, fns, max(4, launches // div))

@@ -8,7 +8,7 @@ autograd, see ``tests/_util.py``), not by the oracle. Every array is plain
 numeric data (``np.savez``, loadable with ``allow_pickle=False``).
 
 Fixtures
-  c1_fwd_fp32.npz      BASELINE config 1: x (2,64,512), weight (64,4), bias (64),
+  c1_fwd_fp32.npz      benchmark configuration C1: x (2,64,512), weight (64,4), bias (64),
                        N(0,1) from seed 0 in that order, SiLU -> out
   bwd_init_fp32.npz    (2,16,64) W4, bias, SiLU, initial_states, dout, dfinal_states
                        -> dx (with the final-states tail), dweight, dbias, dinitial_states

@@ -1,4 +1,4 @@
-"""BASELINE.json configurations at full size.
+"""The benchmark configurations C1-C5 at full size.
 
 At these sizes every output is checked against a float64 closed form
 computed with torch on the GPU (shifted products and sums: the plain-torch

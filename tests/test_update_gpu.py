@@ -5,7 +5,7 @@ state; both the outputs and the mutated conv_state are compared.
 Coverage follows the reference's tests/test_update.py: single token with
 state_len = W-1, short bursts, decode loop == full forward (bit-exact for
 fp16/bf16), circular buffer incl. cache_seqlens >= state_len, circular decode
-loop, conv_state_indices pools, padding (-1) rows, plus the BASELINE decode
+loop, conv_state_indices pools, padding (-1) rows, plus the benchmark decode
 shapes at reduced batch and out-of-pool indices.
 """
 
@@ -194,7 +194,7 @@ def test_strided_inputs(dtype):
 
 @pytest.mark.parametrize("seqlen,S,circular", [(1, 3, False), (4, 64, True)])
 def test_baseline_decode_shapes_reduced(seqlen, S, circular):
-    """BASELINE config 4 with batch 32 (full size runs in tests/test_configs_gpu.py)."""
+    """Benchmark configuration C4 with batch 32 (full size runs in tests/test_configs_gpu.py)."""
     g = torch.Generator().manual_seed(0)
     B, D, W = 32, 5120, 4
     x = torch.randn(B, D, seqlen, generator=g).bfloat16()
