@@ -64,7 +64,8 @@ int cc1d_bwd(const cc1d_bwd_params* p, void* stream) {
     if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
     if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
     if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
-    if (p->seq_idx != nullptr && (p->initial_states != nullptr || p->dfinal_states != nullptr))
+    if (p->seq_idx != nullptr &&
+        (p->initial_states != nullptr || p->dfinal_states != nullptr || p->dinitial_states != nullptr))
         return CC1D_ERR_EXCLUSIVE;
     if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -94,7 +95,8 @@ int cc1d_bwd_typed(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stre
     if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
     if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
     if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
-    if (p->seq_idx != nullptr && (p->initial_states != nullptr || p->dfinal_states != nullptr))
+    if (p->seq_idx != nullptr &&
+        (p->initial_states != nullptr || p->dfinal_states != nullptr || p->dinitial_states != nullptr))
         return CC1D_ERR_EXCLUSIVE;
     if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
     const hipStream_t s = static_cast<hipStream_t>(stream);

@@ -31,6 +31,21 @@ template <> __device__ __forceinline__ f16 from_f32<f16>(float v) {
     return f16{__builtin_bit_cast(uint16_t, (_Float16)v)};
 }
 
+// Two fp32 values narrowed into one dword, a in the low half: one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 (RNE, the same rounding as from_f32).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16>(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
 // Round-trip through the storage dtype (what a store followed by a load gives).
 template <typename T> __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
 
@@ -58,15 +73,13 @@ template <> __device__ __forceinline__ u32x4 vpack<float>(const float* f) {
 template <> __device__ __forceinline__ u32x4 vpack<bf16>(const float* f) {
     u32x4 r;
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-        r[d] = (uint32_t)from_f32<bf16>(f[2 * d]).bits | ((uint32_t)from_f32<bf16>(f[2 * d + 1]).bits << 16);
+    for (int d = 0; d < 4; ++d) r[d] = pack2<bf16>(f[2 * d], f[2 * d + 1]);
     return r;
 }
 template <> __device__ __forceinline__ u32x4 vpack<f16>(const float* f) {
     u32x4 r;
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-        r[d] = (uint32_t)from_f32<f16>(f[2 * d]).bits | ((uint32_t)from_f32<f16>(f[2 * d + 1]).bits << 16);
+    for (int d = 0; d < 4; ++d) r[d] = pack2<f16>(f[2 * d], f[2 * d + 1]);
     return r;
 }
 
@@ -150,8 +163,7 @@ template <typename T, int N> struct Lanes {
             for (int i = 0; i < ND; ++i) d[i] = __float_as_uint(f[i]);
         } else {
 #pragma unroll
-            for (int i = 0; i < ND; ++i)
-                d[i] = (uint32_t)from_f32<T>(f[2 * i]).bits | ((uint32_t)from_f32<T>(f[2 * i + 1]).bits << 16);
+            for (int i = 0; i < ND; ++i) d[i] = pack2<T>(f[2 * i], f[2 * i + 1]);
         }
     }
 };

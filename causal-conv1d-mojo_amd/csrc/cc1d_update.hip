@@ -316,7 +316,7 @@ __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, 
             if (d * PER < Ls) {
                 uint32_t v;
                 if constexpr (PER == 1) v = __float_as_uint(o[d]);
-                else v = (uint32_t)from_f32<T>(o[2 * d]).bits | ((uint32_t)from_f32<T>(o[2 * d + 1 < LMAX ? 2 * d + 1 : 0]).bits << 16);
+                else v = pack2<T>(o[2 * d], o[2 * d + 1 < LMAX ? 2 * d + 1 : 0]);
                 reinterpret_cast<uint32_t*>(orow)[d] = v;
             }
         }

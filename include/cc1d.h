@@ -56,7 +56,8 @@ enum cc1d_status {
     CC1D_ERR_DTYPE = 2,             /* dtype code not in {0, 1, 2} */
     CC1D_ERR_WIDTH = 3,             /* width outside 2..9 */
     CC1D_ERR_SHAPE = 4,             /* negative size, or a size/stride too large for the kernels */
-    CC1D_ERR_EXCLUSIVE = 5,         /* seq_idx given together with initial_states or final_states */
+    CC1D_ERR_EXCLUSIVE = 5,         /* seq_idx given together with initial_states or final_states
+                                       (backward: or with dfinal_states / dinitial_states) */
     CC1D_ERR_STATE_LEN = 6,         /* conv_state length < width - 1 */
     CC1D_ERR_LAUNCH = 7,            /* the HIP runtime refused a kernel launch */
     CC1D_ERR_WORKSPACE = 8          /* workspace smaller than cc1d_bwd_workspace_floats() */
@@ -113,7 +114,7 @@ typedef struct cc1d_bwd_params {
     void* dx;
     float* dweight_acc;            /* (dim, width) fp32, accumulated into */
     float* dbias_acc;              /* (dim,) fp32 or NULL */
-    void* dinitial_states;         /* required when initial_states is given */
+    void* dinitial_states;         /* required when initial_states is given; NULL with seq_idx */
     int64_t batch, dim, seqlen, width;
     int64_t x_stride[3];
     int64_t weight_stride[2];

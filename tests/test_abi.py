@@ -123,6 +123,7 @@ def test_bwd_validation_codes(lib):
     assert call(width=11) == ERR_WIDTH
     assert call(seq_idx=16, initial_states=16, dinitial_states=16) == ERR_EXCL
     assert call(seq_idx=16, dfinal_states=16) == ERR_EXCL
+    assert call(seq_idx=16, dinitial_states=16) == ERR_EXCL
     assert call(initial_states=16) == ERR_NULL  # dinitial_states missing
     assert call() == ERR_NULL
     assert call(batch=0) == OK
@@ -148,6 +149,7 @@ def test_bwd_typed_validation_codes(lib):
     assert call(dtype=-1) == ERR_DTYPE
     assert call(width=11) == ERR_WIDTH
     assert call(seq_idx=16, dfinal_states=16) == ERR_EXCL
+    assert call(seq_idx=16, dinitial_states=16) == ERR_EXCL
     assert call(initial_states=16) == ERR_NULL  # dinitial_states missing
     assert call() == ERR_NULL  # dweight missing
     assert call(gkw=dict(dweight=16)) == ERR_NULL  # x, dout, dx, workspace missing
