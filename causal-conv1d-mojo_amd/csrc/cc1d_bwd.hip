@@ -125,7 +125,8 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         float dfin[H];
 #pragma unroll
         for (int i = 0; i < H; ++i) dfin[i] = 0.0f;
-        if (p.dfinal_states != nullptr && tn >= L) {
+        const bool dfin_row = p.dfinal_states != nullptr && tn >= L;
+        if (dfin_row) {
             const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
                            c * p.dfinal_states_stride[1];
 #pragma unroll
@@ -277,9 +278,15 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
             }
             // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
             // here, so the W-1 tail positions are the end of the last vector.
-            if (p.dfinal_states != nullptr && t + EPV == L) {
+            // A wave-uniform branch skips it for every segment without the row
+            // end (as a lane-masked block it was issued, empty, by all of them).
+            if (dfin_row) {
+                const bool last = t + EPV == L;
 #pragma unroll
-                for (int i = EPV - H; i < EPV; ++i) o[i] = round_to<T>(o[i]) + dfin[H - EPV + i];
+                for (int i = EPV - H; i < EPV; ++i) {
+                    const float v = round_to<T>(o[i]) + dfin[H - EPV + i];
+                    o[i] = last ? v : o[i];
+                }
             }
             if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
         }
