@@ -15,7 +15,7 @@
 //
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
-//                   fwd_rows_vec (one wavefront per block).
+//                   fwd_rows_vec (one item per wavefront, 4 per block).
 //   bwd_cl       -- channel-last (unit channel stride); a lane owns 4 bytes of
 //                   adjacent channels, a wavefront a tile of time steps.
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
@@ -32,6 +32,8 @@ struct BwdArgs {
     int64_t groups;   // cl: channel groups of 64 * CPL
 };
 
+// channel-first rows: (row, segment) items per block, one per wavefront
+constexpr int kRowsWPB = 4;
 // channel-last launch shape: time steps per wavefront tile, tiles per block
 constexpr int kClTS = 16;
 constexpr int kClWPB = 4;
@@ -315,18 +317,18 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
     bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
 }
 
-// One wavefront per block; item = (row, segment) with row = b * dim + c, in
-// memory order like the forward, so consecutive blocks stream consecutive
-// rows. The wavefront reduces its weight/bias-gradient partials with a
+// One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
+// segment) with row = b * dim + c, in memory order like the forward, so
+// consecutive wavefronts stream consecutive rows. The wavefront reduces its weight/bias-gradient partials with a
 // ds_bpermute butterfly and lanes 0..W add them to the fp32 accumulators
 // (one atomic instruction). All index arithmetic is 32-bit (the launcher
 // checks the ranges).
 template <typename T, int W, int VPT, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(64) bwd_rows_vec(const BwdArgs a) {
+__global__ void __launch_bounds__(64 * kRowsWPB) bwd_rows_vec(const BwdArgs a) {
     constexpr int SEG = 64 * VPT * elems16<T>::value;
     const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x;
-    const uint32_t item = uniform32(blockIdx.x);
+    const int lane = threadIdx.x & 63;
+    const uint32_t item = uniform32(blockIdx.x * (uint32_t)kRowsWPB + (threadIdx.x >> 6));
     if (item >= (uint32_t)a.n_items) return;
     const uint32_t nseg = (uint32_t)a.nseg;
     const uint32_t row = item / nseg;
@@ -825,7 +827,7 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
         pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
         pl.a.n_items = p.batch * p.dim * pl.a.nseg;
-        pl.blocks = pl.a.n_items;
+        pl.blocks = ceil_div(pl.a.n_items, (int64_t)kRowsWPB);
         pl.records = pl.a.n_items;
         return pl;
     }
@@ -859,9 +861,9 @@ int launch_plan(BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream) {
         if constexpr (W - 1 <= elems16<T>::value) {
             return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                 constexpr bool SEQ = decltype(qc)::value;
-                if (pl.vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
-                else if (pl.vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
-                else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64, 0, stream>>>(a);
+                if (pl.vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
+                else if (pl.vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
+                else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
                 return launch_status();
             });
         }

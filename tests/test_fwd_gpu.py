@@ -167,6 +167,21 @@ def test_seq_idx(pattern, dtype, activation):
     assert_close(gpu, ref, dtype, name=pattern)
 
 
+@pytest.mark.parametrize("mode", ["no_grad", "inference_mode"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+def test_seq_idx_inference_with_grad_inputs(dtype, mode):
+    """Inference on inputs that require grad (reference tests/test_fwd.py:370-383): no
+    autograd node is built, the output matches the oracle and requires no grad."""
+    x, w, _, _ = make_inputs(1, 16, 32, 4, dtype=dtype)
+    s = seq_pattern("random_runs", 1, 32)
+    xg, wg = x.to(DEV).requires_grad_(), w.to(DEV).requires_grad_()
+    ctx = torch.no_grad() if mode == "no_grad" else torch.inference_mode()
+    with ctx:
+        out = cc.causal_conv1d_fn(xg, wg, seq_idx=s.to(DEV), activation=None)
+    assert not out.requires_grad
+    assert_close(out.cpu(), O.causal_conv1d_fn(x, w, None, seq_idx=s, activation=None), dtype)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("width", [2, 3, 4, 5])
 @pytest.mark.parametrize("seqlen", [64, 4096 + 64, 77])
