@@ -8,10 +8,13 @@
 //   dw[k]  += sum_t dpre[t] * xx(t+k-(W-1)), same gate as the forward
 //   db     += sum_t dpre[t]
 //   dinit[i] = sum_{k<=i} w[k] * dpre[i-k]   (i < W-1)
-// dweight/dbias are reduced in fp32: per lane, across the wavefront
-// (ds_bpermute butterfly), then one fp32 atomic add per (wavefront, tap)
-// into the caller's zeroed accumulator -- as in the reference, the order of
-// those adds (over batches and segments) is not fixed.
+// dweight/dbias are reduced in fp32: per lane, then across the wavefront
+// (row kernels: ds_bpermute butterfly) or the block (channel-last: LDS).
+// cc1d_bwd adds the sums into the caller's zeroed fp32 accumulators with
+// atomics -- as in the reference, the order of those adds (over batches and
+// segments) is not fixed. cc1d_bwd_typed writes them as partial records
+// instead, and bwd_reduce adds each channel's records in a fixed order and
+// rounds once to the dtype.
 //
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
