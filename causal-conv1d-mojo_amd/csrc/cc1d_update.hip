@@ -16,8 +16,9 @@
 //                     channels of 2 batch entries, so x, out, weight and the
 //                     (EPV x S) state blocks move as 16-byte vectors.
 //   update_circ_vec -- circular mode on contiguous state lines of whole
-//                     16-byte chunks: one thread per (b, c) reads and writes
-//                     the one or two chunks that hold its window.
+//                     16-byte chunks: two adjacent lanes per (b, c) read the
+//                     two chunks that hold its window (one 32-byte access),
+//                     swap them, and write back the ones the window touches.
 //   update_circ    -- other circular cases with up to 8 new tokens; one thread
 //                     per (b, c) with all loads issued before any store.
 //   update_generic -- everything else; one thread per (b, c).
@@ -268,23 +269,24 @@ template <typename T> __device__ __forceinline__ uint32_t raw_bits(const T* p) {
 
 // Circular mode on contiguous, 16-byte aligned state lines whose length is a
 // multiple of the 16-byte chunk (EPV elements), with a window of W-1 history
-// plus Ls new positions that spans at most two chunks. One thread per (b, c),
-// lanes on adjacent channels. The window starts at offset O (compile-time)
-// inside its first chunk, so every element access is a register access; the
-// thread reads the one or two chunks of its window as 16-byte vectors, writes
-// the new tokens into them and stores them back whole (the other positions
-// of a chunk are written back unchanged; only this thread touches this state
-// line).
+// plus Ls new positions that spans at most two chunks: ka and the chunk kb
+// after it. Two adjacent lanes per (b, c): the lead lane reads chunk ka, its
+// partner chunk kb -- one 32-byte access when kb follows ka in memory -- and
+// they swap the chunks, so both hold the window. The window starts at offset
+// O (compile-time) inside ka, so every element access is a register access.
+// Both lanes write the new tokens into their copies and compute the outputs;
+// the lead lane writes the outputs and stores chunk ka back whole, the
+// partner stores chunk kb when the window reaches into it (the other
+// positions of a chunk are written back unchanged; only this pair touches
+// this state line).
 template <typename T, int W, bool SILU, bool DW, int O>
 __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, uint32_t b, uint32_t c, T* sl,
                                                    int32_t ka, int32_t kb, int Ls, const uint32_t* xb,
-                                                   const float* w, float bias) {
+                                                   const float* w, float bias, u32x4 va, u32x4 vb, bool lead) {
     constexpr int H = W - 1;
     constexpr int EPV = elems16<T>::value;
     constexpr int LMAX = EPV + 1 - H;  // most new tokens a two-chunk window holds
     const bool cross = O + H + Ls > EPV;
-    u32x4 va = vload(sl + ka * EPV);
-    u32x4 vb = vload(sl + kb * EPV);  // unconditional: the loads issue together
 
     float win[W];
 #pragma unroll
@@ -304,7 +306,9 @@ __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, 
             float acc = conv_taps<W>(bias, w, win);
             if constexpr (SILU) acc = silu(acc);
             o[i] = acc;
-            if constexpr (!DW) st(orow, i * p.out_stride[2], acc);
+            if constexpr (!DW) {
+                if (lead) st(orow, i * p.out_stride[2], acc);
+            }
 #pragma unroll
             for (int k = 0; k < H; ++k) win[k] = win[k + 1];
         }
@@ -313,7 +317,7 @@ __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, 
         constexpr int PER = 4 / (int)sizeof(T);
 #pragma unroll
         for (int d = 0; d < (LMAX + PER - 1) / PER; ++d) {
-            if (d * PER < Ls) {
+            if (lead && d * PER < Ls) {
                 uint32_t v;
                 if constexpr (PER == 1) v = __float_as_uint(o[d]);
                 else v = pack2<T>(o[2 * d], o[2 * d + 1 < LMAX ? 2 * d + 1 : 0]);
@@ -321,9 +325,12 @@ __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, 
             }
         }
     }
-    vstore(sl + ka * EPV, va);
-    if (cross) vstore(sl + kb * EPV, vb);
+    if (lead) vstore(sl + ka * EPV, va);
+    else if (cross) vstore(sl + kb * EPV, vb);
 }
+
+// DPP quad_perm [1, 0, 3, 2]: each lane reads its pair partner (lane ^ 1)
+constexpr int kQuadSwapPairs = 1 | (0 << 2) | (3 << 4) | (2 << 6);
 
 template <typename T, int W, bool SILU, bool DW>
 __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
@@ -332,8 +339,10 @@ __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
     constexpr int LMAX = EPV + 1 - H;
     static_assert(LMAX >= 1, "window must fit in two chunks");
     const cc1d_update_params& p = a.p;
-    const uint32_t idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (uint32_t)a.n_items) return;
+    const uint32_t tid = blockIdx.x * 256 + threadIdx.x;
+    if (tid >= (uint32_t)a.n_items) return;  // n_items is even: a pair leaves together
+    const uint32_t idx = tid >> 1;           // (b, c)
+    const bool lead = (tid & 1u) == 0;
     const uint32_t D = (uint32_t)p.dim;
     const uint32_t b = idx / D;
     const uint32_t c = idx - b * D;
@@ -362,9 +371,11 @@ __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
     const float bias = p.bias ? ld(static_cast<const T*>(p.bias), (int64_t)c * p.bias_stride) : 0.0f;
 
     const int64_t row = state_row(p, b);
-    if (row < 0) {
-        T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
-        for (int i = 0; i < Ls; ++i) st(orow, i * p.out_stride[2], 0.0f);
+    if (row < 0) {  // the same for both lanes of a pair
+        if (lead) {
+            T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+            for (int i = 0; i < Ls; ++i) st(orow, i * p.out_stride[2], 0.0f);
+        }
         return;
     }
     const int32_t S = (int32_t)p.state_len;
@@ -375,18 +386,27 @@ __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
     if (p0 < 0) p0 += S;
     const int32_t ka = p0 / EPV;
     const int32_t kb = ka + 1 < S / EPV ? ka + 1 : 0;  // the chunk after ka, cyclically
+    // each lane of the pair reads one chunk; a quad-permute DPP move (lanes
+    // 0<->1, 2<->3) hands each the other's
+    const u32x4 mine = vload(sl + (lead ? ka : kb) * EPV);
+    u32x4 other;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        other[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mine[i], kQuadSwapPairs, 0xf, 0xf, false);
+    const u32x4 va = lead ? mine : other;
+    const u32x4 vb = lead ? other : mine;
     switch (p0 % EPV) {
-        case 0: update_circ_chunks<T, W, SILU, DW, 0>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-        case 1: update_circ_chunks<T, W, SILU, DW, 1>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-        case 2: update_circ_chunks<T, W, SILU, DW, 2>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-        case 3: update_circ_chunks<T, W, SILU, DW, 3>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+        case 0: update_circ_chunks<T, W, SILU, DW, 0>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+        case 1: update_circ_chunks<T, W, SILU, DW, 1>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+        case 2: update_circ_chunks<T, W, SILU, DW, 2>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+        case 3: update_circ_chunks<T, W, SILU, DW, 3>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
         default:
             if constexpr (EPV == 8) {
                 switch (p0 % EPV) {
-                    case 4: update_circ_chunks<T, W, SILU, DW, 4>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-                    case 5: update_circ_chunks<T, W, SILU, DW, 5>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-                    case 6: update_circ_chunks<T, W, SILU, DW, 6>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
-                    default: update_circ_chunks<T, W, SILU, DW, 7>(p, b, c, sl, ka, kb, Ls, xb, w, bias); break;
+                    case 4: update_circ_chunks<T, W, SILU, DW, 4>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+                    case 5: update_circ_chunks<T, W, SILU, DW, 5>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+                    case 6: update_circ_chunks<T, W, SILU, DW, 6>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
+                    default: update_circ_chunks<T, W, SILU, DW, 7>(p, b, c, sl, ka, kb, Ls, xb, w, bias, va, vb, lead); break;
                 }
             }
             break;
@@ -423,7 +443,7 @@ bool circ_vec_ok(const cc1d_update_params& p) {
     if (p.state_len % EPV != 0 || p.state_len < 2 * EPV) return false;
     if (p.conv_state_stride[2] != 1 || p.conv_state_stride[1] % EPV || p.conv_state_stride[0] % EPV) return false;
     if (!aligned16(p.conv_state)) return false;
-    if (p.batch * p.dim >= ((int64_t)1 << 31) || p.state_len >= ((int64_t)1 << 31)) return false;
+    if (2 * p.batch * p.dim >= ((int64_t)1 << 31) || p.state_len >= ((int64_t)1 << 31)) return false;
     return true;
 }
 
@@ -460,8 +480,10 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                 const dim3 grid((unsigned)ceil_div(a.n_items, 256));
                 if constexpr (W - 1 <= EPV) {
                     if (circ_vec_ok<T>(p)) {
+                        a.n_items = 2 * p.batch * p.dim;  // two lanes per (b, c)
                         return with_flag(circ_dwords_ok<T>(p), [&](auto dc) {
-                            update_circ_vec<T, W, SILU, decltype(dc)::value><<<grid, 256, 0, stream>>>(a);
+                            update_circ_vec<T, W, SILU, decltype(dc)::value>
+                                <<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
                             return launch_status();
                         });
                     }
