@@ -255,12 +255,33 @@ __device__ __forceinline__ int32_t lane_get(int32_t v, int src) {
     return __builtin_amdgcn_ds_bpermute(src << 2, v);
 }
 
-// Sum over the 64 lanes of a wavefront; every lane receives the total.
+// DPP controls (GFX9 encoding) for the wavefront reduction below.
+constexpr int kDppQuadSwap1 = 0xb1;   // quad_perm [1, 0, 3, 2]
+constexpr int kDppQuadSwap2 = 0x4e;   // quad_perm [2, 3, 0, 1]
+constexpr int kDppRowRor4 = 0x124;    // row_ror:4 (rotate within 16 lanes)
+constexpr int kDppRowRor8 = 0x128;    // row_ror:8
+constexpr int kDppRowBcast15 = 0x142; // row_bcast:15 (lane 15 of a row into the next row)
+constexpr int kDppRowBcast31 = 0x143; // row_bcast:31 (lane 31 into rows 2 and 3)
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f32(float v) {
+    // rows outside ROW_MASK receive 0 (the `old` operand), so `v + dpp` leaves them unchanged
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wavefront, returned wave-uniform (every lane
+// receives it). Cross-lane moves are DPP modifiers on VALU adds -- no LDS
+// round trips: sums within quads, then rows of 16, then rows 0+1 and 2+3 into
+// rows 1 and 3, then rows 0+1 into rows 2 and 3; lane 63 holds the total.
+// All 64 lanes must be active.
 __device__ __forceinline__ float wave_sum(float v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += lane_get(v, lane ^ m);
-    return v;
+    v += dpp_f32<kDppQuadSwap1, 0xf>(v);
+    v += dpp_f32<kDppQuadSwap2, 0xf>(v);
+    v += dpp_f32<kDppRowRor4, 0xf>(v);
+    v += dpp_f32<kDppRowRor8, 0xf>(v);
+    v += dpp_f32<kDppRowBcast15, 0xa>(v);
+    v += dpp_f32<kDppRowBcast31, 0xc>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Wavefront-uniform value (lets the compiler keep it in an SGPR).
