@@ -9,7 +9,7 @@
 //   db     += sum_t dpre[t]
 //   dinit[i] = sum_{k<=i} w[k] * dpre[i-k]   (i < W-1)
 // dweight/dbias are reduced in fp32: per lane, then across the wavefront
-// (row kernels: ds_bpermute butterfly) or the block (channel-last: LDS).
+// (row kernels: DPP adds) or the block (channel-last: LDS).
 // cc1d_bwd adds the sums into the caller's zeroed fp32 accumulators with
 // atomics -- as in the reference, the order of those adds (over batches and
 // segments) is not fixed. cc1d_bwd_typed writes them as partial records
@@ -322,10 +322,10 @@ __device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int l
 
 // One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
 // segment) with row = b * dim + c, in memory order like the forward, so
-// consecutive wavefronts stream consecutive rows. The wavefront reduces its weight/bias-gradient partials with a
-// ds_bpermute butterfly and lanes 0..W add them to the fp32 accumulators
-// (one atomic instruction). All index arithmetic is 32-bit (the launcher
-// checks the ranges).
+// consecutive wavefronts stream consecutive rows. The wavefront sums its
+// weight/bias-gradient partials with DPP adds, and lanes 0..W add them to
+// the fp32 accumulators (one atomic instruction) or write the item's partial
+// record. All index arithmetic is 32-bit (the launcher checks the ranges).
 template <typename T, int W, int VPT, bool SILU, bool SEQ>
 __global__ void __launch_bounds__(64 * kRowsWPB) bwd_rows_vec(const BwdArgs a) {
     constexpr int SEG = 64 * VPT * elems16<T>::value;
