@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(256) update_generic(const UpdArgs a) {
 // past the batch or padding entries read row 0 / entry 0) before the
 // arithmetic; only the stores are predicated. Lanes run along channels, so
 // x, out and the (EPV x S) state blocks of one entry are contiguous spans.
-template <typename T, int W, bool SILU, int BPL>
+template <typename T, int W, bool SILU, int BPL, bool UB>
 __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
@@ -121,7 +121,9 @@ __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= (uint32_t)a.n_items) return;
     const uint32_t ng = (uint32_t)a.ngroups;
-    const uint32_t b0 = (idx / ng) * BPL;
+    // UB: ngroups is a multiple of 64, so a wavefront never straddles two
+    // batch entries; b0 is then wave-uniform and the pool indices are scalar loads
+    const uint32_t b0 = UB ? uniform32((idx / ng) * BPL) : (idx / ng) * BPL;
     const uint32_t c0 = (idx - (idx / ng) * ng) * EPV;
     const uint32_t nb = (uint32_t)p.batch;
 
@@ -138,7 +140,7 @@ __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
         const uint32_t b = b0 + q < nb ? b0 + q : 0;
         int32_t r = (int32_t)b;
         if (p.conv_state_indices != nullptr) {
-            r = p.conv_state_indices[b];
+            r = UB ? ld_uniform(p.conv_state_indices + b) : p.conv_state_indices[b];
             if (r >= p.state_rows) r = -1;
         }
         row[q] = (b0 + q < nb) ? r : -2;
@@ -473,8 +475,11 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                     constexpr int BPL = 2;
                     a.ngroups = p.dim / EPV;
                     a.n_items = ceil_div(p.batch, BPL) * a.ngroups;
-                    update_vec1<T, W, SILU, BPL><<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
-                    return launch_status();
+                    return with_flag(a.ngroups % 64 == 0, [&](auto ub) {
+                        update_vec1<T, W, SILU, BPL, decltype(ub)::value>
+                            <<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
+                        return launch_status();
+                    });
                 }
                 a.n_items = p.batch * p.dim;
                 const dim3 grid((unsigned)ceil_div(a.n_items, 256));

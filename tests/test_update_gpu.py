@@ -138,7 +138,7 @@ def test_circular_chunked_lines(dtype, width, seqlen, S):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("circular", [False, True])
-@pytest.mark.parametrize("dim", [16, 64])
+@pytest.mark.parametrize("dim", [16, 64, 512])  # 512: whole wavefronts per batch entry (scalar index reads)
 def test_conv_state_indices_pool(dtype, circular, dim):
     x, w, b, _ = make_inputs(3, dim, 1, 4, dtype=dtype)
     S = 3 if not circular else 7
@@ -155,7 +155,7 @@ def test_conv_state_indices_pool(dtype, circular, dim):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
-@pytest.mark.parametrize("dim", [8, 64])
+@pytest.mark.parametrize("dim", [8, 64, 1024])  # 1024: whole wavefronts per batch entry (scalar index reads)
 def test_padding_and_out_of_pool_rows(dtype, dim):
     x, w, b, _ = make_inputs(4, dim, 1, 4, dtype=dtype)
     pool = make_inputs(4, dim, 3, 4, dtype=dtype, seed=1)[0]
