@@ -549,11 +549,10 @@ __device__ __forceinline__ int32_t cl_window_id(const int32_t* sr, int32_t ss1, 
 }
 
 // dpre, dx (+ dfinal tail, dinitial_states) and the weight/bias-gradient
-// partials of a loaded tile. G: apply the seq_idx equality gate with the
-// window ids id[0 .. NX-1] (wave-uniform).
-template <typename T, int W, int CPL, int TS, bool SILU, bool G>
+// partials of a loaded tile whose rows belong to one sequence.
+template <typename T, int W, int CPL, int TS, bool SILU>
 __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
-                                               bool active, const ClTile<T, W, CPL, TS>& r, const int32_t* id,
+                                               bool active, const ClTile<T, W, CPL, TS>& r,
                                                ClPartials<W, CPL>& out) {
     using Tile = ClTile<T, W, CPL, TS>;
     constexpr int H = W - 1;
@@ -585,20 +584,15 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
             if constexpr (SILU) {
                 float q = bq[e];
 #pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (!G || id[j + k] == id[j + H]) q = __builtin_fmaf(wq[k][e], r.xv[j + k].get(e), q);
+                for (int k = 0; k < W; ++k) q = __builtin_fmaf(wq[k][e], r.xv[j + k].get(e), q);
                 d = silu_bwd_q(gval, q);
             }
             if (t >= L) d = 0.0f;
-            if constexpr (G) {
-                if (id[j + H] < 0) d = 0.0f;
-            }
             dp[j][e] = d;
             if (j < TS) {
                 out.pb[e] += d;
 #pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (!G || id[j + k] == id[j + H]) out.pw[k][e] = __builtin_fmaf(d, r.xv[j + k].get(e), out.pw[k][e]);
+                for (int k = 0; k < W; ++k) out.pw[k][e] = __builtin_fmaf(d, r.xv[j + k].get(e), out.pw[k][e]);
             }
         }
     }
@@ -611,8 +605,7 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
         for (int e = 0; e < CPL; ++e) {
             float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < W; ++k)
-                if (!G || id[j + H + k] == id[j + H]) acc = __builtin_fmaf(w[H - k][e], dp[j + k][e], acc);
+            for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[H - k][e], dp[j + k][e], acc);
             o[e] = acc;
         }
         if (p.dfinal_states != nullptr && t >= L - m && t < L && active) {
@@ -641,6 +634,128 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
                 for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], dp[i - k][e], acc);
                 st(di, i * p.dinitial_states_stride[2], acc);
             }
+        }
+    }
+}
+
+// A tile whose window holds a seq_idx boundary: the same arithmetic with the
+// equality gate, one time step per iteration of a rolled loop. x and dout
+// rows are read again (the tile's own loads have just brought them into the
+// cache), PD rows ahead of the one in use; the last W rows of x, dpre and
+// their ids slide in registers. Unrolled over the tile's registers, the gated
+// arithmetic needs ~40 more VGPRs than the ungated one, and because both
+// live in one kernel, every tile would run at the lower occupancy. seq_idx
+// excludes initial_states, dfinal_states and dinitial_states (the entry
+// points reject the combination), so none of them appears here.
+template <typename T, int W, int CPL, int TS, bool SILU>
+__device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
+                                             bool active, int32_t lid, ClPartials<W, CPL>& out) {
+    constexpr int H = W - 1;
+    constexpr int NROW = TS + H;  // dpre rows t0 .. t0+TS+H-1
+    constexpr int PD = 4;         // rows in flight
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
+    const int32_t ds2 = (int32_t)p.dx_stride[2];
+    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
+    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
+    T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
+
+    float w[W][CPL], wq[W][CPL], bq[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+        const int64_t c = active ? c0 + e : 0;
+#pragma unroll
+        for (int k = 0; k < W; ++k) {
+            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+            wq[k][e] = -kLog2e * w[k][e];
+        }
+        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
+    }
+
+    // x row s (and dout row s), zero outside [0, L)
+    auto load_x = [&](int32_t s, Lanes<T, CPL>& xr) {
+        xr.zero();
+        if (active && s >= 0 && s < L) xr.template load<false>(xb + s * xs2);
+    };
+    auto load_row = [&](int32_t s, Lanes<T, CPL>& xr, Lanes<T, CPL>& gr) {
+        load_x(s, xr);
+        gr.zero();
+        if (active && s < L) gr.template load<false>(gb + s * gs2);
+    };
+    float xw[W][CPL], dw[W][CPL];  // x and dpre at positions t-H .. t
+    int32_t iw[W];                 // their ids (-1 outside [0, L))
+#pragma unroll
+    for (int k = 0; k < H; ++k) {
+        Lanes<T, CPL> xr;
+        load_x(t0 - H + k, xr);
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            xw[k + 1][e] = xr.get(e);
+            dw[k + 1][e] = 0.0f;
+        }
+        iw[k + 1] = __builtin_amdgcn_readlane(lid, k);
+    }
+    Lanes<T, CPL> xq[PD], gq[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load_row(t0 + i, xq[i], gq[i]);
+
+#pragma unroll 1
+    for (int j = 0; j < NROW; ++j) {
+        const int32_t t = t0 + j;
+        const Lanes<T, CPL> xr = xq[0], gr = gq[0];
+#pragma unroll
+        for (int i = 0; i + 1 < PD; ++i) {
+            xq[i] = xq[i + 1];
+            gq[i] = gq[i + 1];
+        }
+        if (j + PD < NROW) load_row(t + PD, xq[PD - 1], gq[PD - 1]);
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+            iw[k] = iw[k + 1];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                xw[k][e] = xw[k + 1][e];
+                dw[k][e] = dw[k + 1][e];
+            }
+        }
+        iw[H] = __builtin_amdgcn_readlane(lid, j + H);
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) xw[H][e] = xr.get(e);
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            const float gval = gr.get(e);
+            float d = gval;
+            if constexpr (SILU) {
+                float q = bq[e];
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (iw[k] == iw[H]) q = __builtin_fmaf(wq[k][e], xw[k][e], q);
+                d = silu_bwd_q(gval, q);
+            }
+            if (t >= L || iw[H] < 0) d = 0.0f;
+            dw[H][e] = d;
+            if (j < TS) {
+                out.pb[e] += d;
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (iw[k] == iw[H]) out.pw[k][e] = __builtin_fmaf(d, xw[k][e], out.pw[k][e]);
+            }
+        }
+        // dx at position t - H: dpre rows t-H .. t, tap k kept when id(t-H+k) == id(t-H)
+        const int32_t s = t - H;
+        if (j >= H && active && s < L) {
+            float o[CPL];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int k = 0; k < W; ++k)
+                    if (iw[k] == iw[0]) acc = __builtin_fmaf(w[H - k][e], dw[k][e], acc);
+                o[e] = acc;
+            }
+            Lanes<T, CPL> ov;
+            ov.set(o);
+            ov.template store<true>(dxb + s * ds2);
         }
     }
 }
@@ -683,18 +798,16 @@ __global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
         Tile r;
         cl_bwd_load<T, W, CPL, TS>(p, b, t0, c0, active, r);
         bool one_id = true;
-        int32_t id[Tile::NX];
+        int32_t lid = 0;
         if constexpr (SEQ) {
             const int32_t s = t0 - H + lane;
-            const int32_t lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0],
-                                                       (int32_t)p.seq_idx_stride[1], L, t0, H, lane);
+            lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0], (int32_t)p.seq_idx_stride[1], L, t0,
+                                         H, lane);
             const int32_t id_cur = __builtin_amdgcn_readlane(lid, H);
             one_id = id_cur >= 0 && __ballot(lane < Tile::NX && s >= 0 && s < L && lid != id_cur) == 0;
-#pragma unroll
-            for (int i = 0; i < Tile::NX; ++i) id[i] = __builtin_amdgcn_readlane(lid, i);
         }
-        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU, false>(p, b, t0, c0, active, r, id, part);
-        else if constexpr (SEQ) cl_bwd_compute<T, W, CPL, TS, SILU, true>(p, b, t0, c0, active, r, id, part);
+        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU>(p, b, t0, c0, active, r, part);
+        else if constexpr (SEQ) cl_bwd_gated<T, W, CPL, TS, SILU>(p, b, t0, c0, active, lid, part);
     }
 
     // ---- weight / bias gradient: sum the block's tiles in LDS, then

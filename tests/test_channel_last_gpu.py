@@ -81,13 +81,13 @@ def test_cl_forward_states(dtype, width, seqlen):
     assert_equal(fs.cpu(), rfs, name="final_states")
 
 
-def _grads(x, w, b, dout, *, init=None, seq_idx=None, dfs=None):
+def _grads(x, w, b, dout, *, init=None, seq_idx=None, dfs=None, activation="silu"):
     """Autograd through a channel-last view; gradients come back as (B, D, L) values."""
     base = x.transpose(1, 2).contiguous().to(DEV).requires_grad_()
     wg = w.to(DEV).requires_grad_()
     bg = b.to(DEV).requires_grad_()
     ig = init.to(DEV).requires_grad_() if init is not None else None
-    kw = dict(initial_states=ig, activation="silu", seq_idx=None if seq_idx is None else seq_idx.to(DEV))
+    kw = dict(initial_states=ig, activation=activation, seq_idx=None if seq_idx is None else seq_idx.to(DEV))
     if dfs is not None:
         out, fs = cc.causal_conv1d_fn(base.transpose(1, 2), wg, bg, return_final_states=True, **kw)
         torch.autograd.backward([out, fs], [dout.to(DEV), dfs.to(DEV)])
@@ -126,6 +126,19 @@ def test_cl_backward_seq_idx(pattern, dtype, width, seqlen):
     dout = make_inputs(2, 130, seqlen, width, dtype=dtype, seed=1)[0]
     s = seq_pattern(pattern, 2, seqlen)
     _check(_grads(x, w, b, dout, seq_idx=s), O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype)
+
+
+@pytest.mark.parametrize("dtype,width", list(_fwd_cases()))
+@pytest.mark.parametrize("pattern", ["with_padding", "repeat_ids", "random_runs"])
+@pytest.mark.parametrize("activation", [None, "silu"])
+def test_cl_backward_seq_idx_widths(dtype, width, pattern, activation):
+    """Tiles holding a boundary at every width, with and without SiLU; 3 batches and 4 tile
+    groups per row, so boundary tiles sit among ordinary ones in one block."""
+    x, w, b, _ = make_inputs(3, 192, 300, width, dtype=dtype)
+    dout = make_inputs(3, 192, 300, width, dtype=dtype, seed=1)[0]
+    s = seq_pattern(pattern, 3, 300)
+    got = _grads(x, w, b, dout, seq_idx=s, activation=activation)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation=activation), dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
