@@ -639,12 +639,13 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
 }
 
 // A tile whose window holds a seq_idx boundary: the same arithmetic with the
-// equality gate, one time step per iteration of a rolled loop. x and dout
-// rows are read again (the tile's own loads have just brought them into the
-// cache), PD rows ahead of the one in use; the last W rows of x, dpre and
-// their ids slide in registers. Unrolled over the tile's registers, the gated
-// arithmetic needs ~40 more VGPRs than the ungated one, and because both
-// live in one kernel, every tile would run at the lower occupancy. seq_idx
+// equality gate, time step after time step in a rolled loop over batches of
+// G steps. x and dout rows are read again (the tile's own loads have just
+// brought them into the cache), one batch of loads per iteration, used in
+// place; the last W rows of x, dpre and their ids slide in registers.
+// Unrolled over the tile's registers instead, the gated arithmetic took ~40
+// more VGPRs than the ungated one, and because both live in one kernel,
+// every tile ran at the lower occupancy. seq_idx
 // excludes initial_states, dfinal_states and dinitial_states (the entry
 // points reject the combination), so none of them appears here.
 template <typename T, int W, int CPL, int TS, bool SILU>
@@ -652,7 +653,7 @@ __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t 
                                              bool active, int32_t lid, ClPartials<W, CPL>& out) {
     constexpr int H = W - 1;
     constexpr int NROW = TS + H;  // dpre rows t0 .. t0+TS+H-1
-    constexpr int PD = 4;         // rows in flight
+    constexpr int G = 4;          // rows per batch of loads
     const int32_t L = (int32_t)p.seqlen;
     const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
     const int32_t ds2 = (int32_t)p.dx_stride[2];
@@ -695,20 +696,9 @@ __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t 
         }
         iw[k + 1] = __builtin_amdgcn_readlane(lid, k);
     }
-    Lanes<T, CPL> xq[PD], gq[PD];
-#pragma unroll
-    for (int i = 0; i < PD; ++i) load_row(t0 + i, xq[i], gq[i]);
-
-#pragma unroll 1
-    for (int j = 0; j < NROW; ++j) {
+    // one time step: x row t and dout row t enter the windows
+    auto step = [&](int j, const Lanes<T, CPL>& xr, const Lanes<T, CPL>& gr) {
         const int32_t t = t0 + j;
-        const Lanes<T, CPL> xr = xq[0], gr = gq[0];
-#pragma unroll
-        for (int i = 0; i + 1 < PD; ++i) {
-            xq[i] = xq[i + 1];
-            gq[i] = gq[i + 1];
-        }
-        if (j + PD < NROW) load_row(t + PD, xq[PD - 1], gq[PD - 1]);
 #pragma unroll
         for (int k = 0; k < H; ++k) {
             iw[k] = iw[k + 1];
@@ -757,6 +747,16 @@ __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t 
             ov.set(o);
             ov.template store<true>(dxb + s * ds2);
         }
+    };
+    // G rows per batch: their loads are issued together and used in place
+#pragma unroll 1
+    for (int j0 = 0; j0 < NROW; j0 += G) {
+        Lanes<T, CPL> xq[G], gq[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) load_row(t0 + j0 + i, xq[i], gq[i]);
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+            if (j0 + i < NROW) step(j0 + i, xq[i], gq[i]);
     }
 }
 
