@@ -497,6 +497,29 @@ template <int W, int CPL> struct ClPartials {
     float pb[CPL];
 };
 
+// The weights and bias of a lane's channels, kept raw: they are read before
+// the tile and converted where they are used, so no conversion waits for
+// them (memory counters retire in order) ahead of the tile's loads.
+// Without a bias the bias read goes to x's first element (an unconditional
+// load, so no branch waits on it) and bias() returns zero.
+template <typename T, int W, int CPL> struct ClWeights {
+    T w[W][CPL], b[CPL];
+    bool has_bias;
+    __device__ __forceinline__ void load(const cc1d_bwd_params& p, int32_t c0, bool active) {
+        const T* __restrict__ wp = static_cast<const T*>(p.weight);
+        has_bias = p.bias != nullptr;
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            const int64_t c = active ? c0 + e : 0;
+#pragma unroll
+            for (int k = 0; k < W; ++k) w[k][e] = wp[c * p.weight_stride[0] + k * p.weight_stride[1]];
+            const T* bsrc = has_bias ? static_cast<const T*>(p.bias) + c * p.bias_stride : static_cast<const T*>(p.x);
+            b[e] = *bsrc;
+        }
+    }
+    __device__ __forceinline__ float bias(int e) const { return has_bias ? to_f32(b[e]) : 0.0f; }
+};
+
 // Issue the loads of the tile at t0 (rows outside the sequence are zero;
 // rows before 0 come from initial_states when given).
 template <typename T, int W, int CPL, int TS>
@@ -538,14 +561,16 @@ __device__ __forceinline__ void cl_bwd_load(const cc1d_bwd_params& p, uint32_t b
 }
 
 // seq_idx of the tile's x-row window: lane i < NX reads position t0 - H + i
-// (clamped address, -1 outside the row), so the reads are one vector load.
+// at a clamped address, so the reads are one unconditional vector load (no
+// wait until the value is used). A position outside [0, L) carries the id
+// of the nearest position inside; the terms it gates are zero either way
+// (x rows there are zero, dpre rows past the end are zero).
 template <int NX>
 __device__ __forceinline__ int32_t cl_window_id(const int32_t* sr, int32_t ss1, int32_t L, int32_t t0, int32_t H,
                                                 int lane) {
     static_assert(NX <= 64, "the id window must fit in one wavefront");
     const int32_t s = t0 - H + lane;
-    const int32_t v = sr[(s < 0 ? 0 : (s < L ? s : L - 1)) * ss1];
-    return (s >= 0 && s < L) ? v : -1;
+    return sr[(s < 0 ? 0 : (s < L ? s : L - 1)) * ss1];
 }
 
 // dpre, dx (+ dfinal tail, dinitial_states) and the weight/bias-gradient
@@ -553,7 +578,7 @@ __device__ __forceinline__ int32_t cl_window_id(const int32_t* sr, int32_t ss1, 
 template <typename T, int W, int CPL, int TS, bool SILU>
 __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
                                                bool active, const ClTile<T, W, CPL, TS>& r,
-                                               ClPartials<W, CPL>& out) {
+                                               const ClWeights<T, W, CPL>& wt, ClPartials<W, CPL>& out) {
     using Tile = ClTile<T, W, CPL, TS>;
     constexpr int H = W - 1;
     constexpr int ND = Tile::ND;
@@ -564,13 +589,12 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
     float w[W][CPL], wq[W][CPL], bq[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
-        const int64_t c = active ? c0 + e : 0;
 #pragma unroll
         for (int k = 0; k < W; ++k) {
-            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+            w[k][e] = to_f32(wt.w[k][e]);
             wq[k][e] = -kLog2e * w[k][e];
         }
-        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
+        bq[e] = -kLog2e * wt.bias(e);
     }
 
     float dp[ND][CPL];
@@ -650,7 +674,8 @@ __device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_
 // points reject the combination), so none of them appears here.
 template <typename T, int W, int CPL, int TS, bool SILU>
 __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
-                                             bool active, int32_t lid, ClPartials<W, CPL>& out) {
+                                             bool active, int32_t lid, const ClWeights<T, W, CPL>& wt,
+                                             ClPartials<W, CPL>& out) {
     constexpr int H = W - 1;
     constexpr int NROW = TS + H;  // dpre rows t0 .. t0+TS+H-1
     constexpr int G = 4;          // rows per batch of loads
@@ -664,13 +689,12 @@ __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t 
     float w[W][CPL], wq[W][CPL], bq[CPL];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
-        const int64_t c = active ? c0 + e : 0;
 #pragma unroll
         for (int k = 0; k < W; ++k) {
-            w[k][e] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
+            w[k][e] = to_f32(wt.w[k][e]);
             wq[k][e] = -kLog2e * w[k][e];
         }
-        bq[e] = -kLog2e * (p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f);
+        bq[e] = -kLog2e * wt.bias(e);
     }
 
     // x row s (and dout row s), zero outside [0, L)
@@ -684,7 +708,7 @@ __device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t 
         if (active && s < L) gr.template load<false>(gb + s * gs2);
     };
     float xw[W][CPL], dw[W][CPL];  // x and dpre at positions t-H .. t
-    int32_t iw[W];                 // their ids (-1 outside [0, L))
+    int32_t iw[W];                 // their ids
 #pragma unroll
     for (int k = 0; k < H; ++k) {
         Lanes<T, CPL> xr;
@@ -795,19 +819,25 @@ __global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
         for (int k = 0; k < W; ++k) part.pw[k][e] = 0.0f;
     }
     if (t0 < L) {  // tiles past the end only join the block reduction
+        // the window's ids (and the weights) are read before the tile: memory
+        // counters retire in order, so the branch on them waits for these
+        // loads only
+        int32_t lid = 0;
+        if constexpr (SEQ)
+            lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0], (int32_t)p.seq_idx_stride[1], L, t0,
+                                         H, lane);
+        ClWeights<T, W, CPL> wt;
+        wt.load(p, c0, active);
         Tile r;
         cl_bwd_load<T, W, CPL, TS>(p, b, t0, c0, active, r);
         bool one_id = true;
-        int32_t lid = 0;
         if constexpr (SEQ) {
             const int32_t s = t0 - H + lane;
-            lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0], (int32_t)p.seq_idx_stride[1], L, t0,
-                                         H, lane);
             const int32_t id_cur = __builtin_amdgcn_readlane(lid, H);
             one_id = id_cur >= 0 && __ballot(lane < Tile::NX && s >= 0 && s < L && lid != id_cur) == 0;
         }
-        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU>(p, b, t0, c0, active, r, part);
-        else if constexpr (SEQ) cl_bwd_gated<T, W, CPL, TS, SILU>(p, b, t0, c0, active, lid, part);
+        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU>(p, b, t0, c0, active, r, wt, part);
+        else if constexpr (SEQ) cl_bwd_gated<T, W, CPL, TS, SILU>(p, b, t0, c0, active, lid, wt, part);
     }
 
     // ---- weight / bias gradient: sum the block's tiles in LDS, then
