@@ -529,19 +529,30 @@ __device__ __forceinline__ void cl_bwd_load(const cc1d_bwd_params& p, uint32_t b
     constexpr int H = W - 1;
     const int32_t L = (int32_t)p.seqlen;
     const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
-    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
-    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
+    // lanes past the last channel read channel 0 (in bounds) so that every
+    // condition below is wave-uniform; they store nothing and their
+    // partials are dropped
+    const int32_t cr = active ? c0 : 0;
+    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + cr;
+    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + cr;
+    if (t0 >= H && t0 + TS + H <= L) {  // every row of the tile lies inside [0, L)
 #pragma unroll
-    for (int i = 0; i < Tile::NX; ++i) {
-        const int32_t s = t0 - H + i;
-        r.xv[i].zero();
-        if (active && s >= 0 && s < L) r.xv[i].template load<false>(xb + s * xs2);
-    }
+        for (int i = 0; i < Tile::NX; ++i) r.xv[i].template load<false>(xb + (t0 - H + i) * xs2);
 #pragma unroll
-    for (int j = 0; j < Tile::ND; ++j) {
-        const int32_t t = t0 + j;
-        r.gv[j].zero();
-        if (active && t < L) r.gv[j].template load<false>(gb + t * gs2);
+        for (int j = 0; j < Tile::ND; ++j) r.gv[j].template load<false>(gb + (t0 + j) * gs2);
+    } else {
+#pragma unroll
+        for (int i = 0; i < Tile::NX; ++i) {
+            const int32_t s = t0 - H + i;
+            r.xv[i].zero();
+            if (s >= 0 && s < L) r.xv[i].template load<false>(xb + s * xs2);
+        }
+#pragma unroll
+        for (int j = 0; j < Tile::ND; ++j) {
+            const int32_t t = t0 + j;
+            r.gv[j].zero();
+            if (t < L) r.gv[j].template load<false>(gb + t * gs2);
+        }
     }
     if (p.initial_states != nullptr && t0 < H && active) {
 #pragma unroll
@@ -838,6 +849,14 @@ __global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
         }
         if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU>(p, b, t0, c0, active, r, wt, part);
         else if constexpr (SEQ) cl_bwd_gated<T, W, CPL, TS, SILU>(p, b, t0, c0, active, lid, wt, part);
+        if (!active) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                part.pb[e] = 0.0f;
+#pragma unroll
+                for (int k = 0; k < W; ++k) part.pw[k][e] = 0.0f;
+            }
+        }
     }
 
     // ---- weight / bias gradient: sum the block's tiles in LDS, then
