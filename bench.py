@@ -25,8 +25,8 @@ Input sets are rotated so that the data touched between two reuses of a
 buffer exceeds the 256 MB Infinity Cache: every launch streams from HBM.
 
 Modes: --mode bench (default), --mode kernels (eager launch loop of the C2
-forward / backward / C4a update, plus the C3 / C5 / C4b launches unless
---no-configs, for rocprofv3 --kernel-trace / --pmc), --mode copy (a plain
+forward / backward / C4a update, plus the C3 / C5 / C4b / varlen-states
+launches unless --no-configs, for rocprofv3 --kernel-trace / --pmc), --mode copy (a plain
 1 GiB device copy, the calibration kernel for FETCH_SIZE / WRITE_SIZE).
 """
 
@@ -66,7 +66,7 @@ def _parse():
     ap.add_argument("--mode", choices=["bench", "kernels", "copy"], default="bench")
     ap.add_argument("--launches", type=int, default=40, help="launches per kernel timing graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-configs", action="store_true", help="skip the C3/C4b/C5 report lines")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C3/C4b/C5/varlen report lines")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
     ap.add_argument("--settle", type=float, default=0.3,
                     help="seconds of untimed C2 kernels before the first timing (clock ramp)")
@@ -345,6 +345,14 @@ def _config_cases(torch, cc):
     nb = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4
     cases["update_c4b"] = (fns, nb, 1, {"note": "14 of 128 bytes of each state row are touched; DRAM bursts "
                                                 "bound this"})
+    # varlen states: x (8192, 4096) bf16 packing the 8 C3 sequences, state_len W-1
+    xv = torch.randn(L3, D3, generator=g, device="cuda").bfloat16()
+    cu = torch.tensor([0] + cuts.tolist() + [L3], dtype=torch.int32, device="cuda")
+    nseq = cu.numel() - 1
+    st = torch.empty(nseq, W - 1, D3, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
+    cases["varlen_states"] = ([lambda: cc._native.native_varlen_states(xv, cu, st)],
+                              2 * nseq * (W - 1) * D3 * 2 + cu.numel() * 4, 1,
+                              {"note": "gathers 8 x 3 rows of 4096 channels (197 KB each way): launch-bound"})
     return cases
 
 
