@@ -10,7 +10,8 @@ backward go through the public API (causal_conv1d_fn + autograd), so the
 dispatcher's choice among the row, channel-last and generic kernels meets
 shapes that no hand-written case picks. A second sweep does the same for the
 decode update (widths 2..9 for every dtype there): linear or circular buffers,
-with and without a state pool. The case's parameters are in its id.
+with and without a state pool; a third gathers varlen states from random
+packings (empty sequences included). The case's parameters are in its id.
 """
 
 from __future__ import annotations
@@ -188,3 +189,30 @@ def test_random_update(c):
     rout = O.causal_conv1d_update(x, rs, w, b, **kw)
     assert_close(out.cpu(), rout, dtype, name="out")
     assert_equal(sg.cpu(), rs, name="conv_state")
+
+
+def _varlen_case(seed):
+    r = random.Random(90_000 + seed)
+    return dict(seed=seed, n=r.randint(1, 8), D=r.choice([r.randint(1, 40), r.randint(41, 300), 64 * r.randint(1, 8)]),
+                S=r.randint(0, 12), dt=r.choice(list(DT)), maxlen=r.choice([3, 20, 300]), strided=r.random() < 0.3)
+
+
+VARLEN_CASES = [_varlen_case(s) for s in range(60)]
+
+
+@pytest.mark.parametrize("c", VARLEN_CASES, ids=lambda c: (f"s{c['seed']}-{c['dt']}-n{c['n']}D{c['D']}S{c['S']}"
+                                                             f"-max{c['maxlen']}{'-strided' if c['strided'] else ''}"))
+def test_random_varlen_states(c):
+    dtype = DT[c["dt"]]
+    g = torch.Generator().manual_seed(3000 + c["seed"])
+    lens = torch.randint(0, c["maxlen"] + 1, (c["n"],), generator=g)  # zero-length sequences included
+    cu = torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lens, 0)]).to(torch.int32)
+    total = int(cu[-1])
+    x = _rand(g, total, c["D"], dtype=dtype)
+    xg = x.to(DEV)
+    if c["strided"]:  # rows of a wider buffer: a channel stride of 1 and a token stride > dim
+        wide = torch.zeros(total, c["D"] + 5, dtype=dtype, device=DEV)
+        wide[:, 3:3 + c["D"]] = xg
+        xg = wide[:, 3:3 + c["D"]]
+    out = cc.causal_conv1d_varlen_states(xg, cu.to(DEV), state_len=c["S"]).cpu()
+    assert_equal(out, O.varlen_states(x, cu, c["S"]), name="states")
