@@ -5,7 +5,8 @@ Each case draws, from its own seed, batch, dim, seqlen, width (2..9; 2..5 for
 fp32, as the API allows), dtype, layout (contiguous; channel-last view; a slice
 of a larger buffer; every other time step of a buffer), bias, activation and
 one of three modes: plain, seq_idx (random runs, some padded with -1), or
-initial_states with return_final_states and both gradients. Forward and
+initial_states with return_final_states and both gradients; the weight is
+sometimes a transposed view and dout sometimes channel-last. Forward and
 backward go through the public API (causal_conv1d_fn + autograd), so the
 dispatcher's choice among the row, channel-last and generic kernels meets
 shapes that no hand-written case picks. A second sweep does the same for the
@@ -46,12 +47,14 @@ def _fn_case(seed):
         bias=r.random() < 0.7,
         act=r.choice([None, "silu"]),
         mode=mode,
+        wt=r.random() < 0.3,     # weight as the transpose of a (width, dim) tensor
+        dcl=r.random() < 0.3,    # dout in the channel-last layout
     )
 
 
 def _fn_id(c):
     return (f"s{c['seed']}-{c['dt']}-B{c['B']}D{c['D']}L{c['L']}W{c['W']}-{c['layout']}-{c['mode']}"
-            f"-{'bias' if c['bias'] else 'nobias'}-{c['act']}")
+            f"-{'bias' if c['bias'] else 'nobias'}-{c['act']}{'-wT' if c['wt'] else ''}{'-doutcl' if c['dcl'] else ''}")
 
 
 FN_CASES = [_fn_case(s) for s in range(360)]
@@ -108,16 +111,22 @@ def test_random_forward_backward(c):
 
     base, view = _device_view(x, c["layout"])
     base.requires_grad_()
-    wg = w.to(DEV).requires_grad_()
+    if c["wt"]:
+        wg = w.t().contiguous().to(DEV).requires_grad_()
+        wv = wg.t()
+    else:
+        wg = w.to(DEV).requires_grad_()
+        wv = wg
+    dg = dout.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) if c["dcl"] else dout.to(DEV)
     bg = b.to(DEV).requires_grad_() if b is not None else None
     ig = init.to(DEV).requires_grad_() if init is not None else None
     kw = dict(activation=c["act"], seq_idx=None if seq is None else seq.to(DEV), initial_states=ig)
     if c["mode"] == "states":
-        out, fs = cc.causal_conv1d_fn(view(base), wg, bg, return_final_states=True, **kw)
-        torch.autograd.backward([out, fs], [dout.to(DEV), dfs.to(DEV)])
+        out, fs = cc.causal_conv1d_fn(view(base), wv, bg, return_final_states=True, **kw)
+        torch.autograd.backward([out, fs], [dg, dfs.to(DEV)])
     else:
-        out = cc.causal_conv1d_fn(view(base), wg, bg, **kw)
-        out.backward(dout.to(DEV))
+        out = cc.causal_conv1d_fn(view(base), wv, bg, **kw)
+        out.backward(dg)
     torch.cuda.synchronize()
 
     ref = O.causal_conv1d_fn(x, w, b, seq_idx=seq, initial_states=init,
@@ -129,7 +138,7 @@ def test_random_forward_backward(c):
     rdx, rdw, rdb, rdi = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=seq, initial_states=init,
                                              dfinal_states=dfs, activation=c["act"])
     assert_close(view(base.grad).cpu(), rdx, dtype, name="dx")
-    assert_reduction_close(wg.grad.cpu(), rdw, dtype, name="dweight")
+    assert_reduction_close(wg.grad.t().cpu() if c["wt"] else wg.grad.cpu(), rdw, dtype, name="dweight")
     if b is not None:
         assert_reduction_close(bg.grad.cpu(), rdb, dtype, name="dbias")
     if init is not None:
