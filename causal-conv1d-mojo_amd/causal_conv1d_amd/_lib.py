@@ -14,7 +14,7 @@ import os
 from pathlib import Path
 
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -73,7 +73,7 @@ class VarlenParams(ctypes.Structure):
         ("x", _vp), ("cu_seqlens", _vp), ("states", _vp),
         ("total_tokens", _i64), ("dim", _i64), ("batch", _i64), ("state_len", _i64),
         ("x_stride", _i64x2), ("states_stride", _i64x3),
-        ("dtype", _i32), ("reserved", _i32),
+        ("dtype", _i32), ("elem_bytes", _i32),
     ]
 
 

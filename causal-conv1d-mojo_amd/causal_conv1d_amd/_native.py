@@ -149,5 +149,7 @@ def native_varlen_states(x, cu_seqlens, states) -> None:
     p.batch, _, p.state_len = states.shape
     _set2(p.x_stride, x)
     _set3(p.states_stride, states)
-    p.dtype = _DTYPE_CODE[x.dtype]
+    # a bit-for-bit copy: any element type, by its size
+    p.dtype = _DTYPE_CODE.get(x.dtype, 0)
+    p.elem_bytes = x.element_size()
     _lib.check(lib.cc1d_varlen_states(ctypes.byref(p), _stream(x)))

@@ -5,14 +5,15 @@ Drop-in for ``src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-67`` (same
 signature, same output shape / dtype / strides, same ``_ref`` alias). The
 reference loops over the batch in Python with one strided torch copy per
 sequence; here one HIP gather kernel writes the whole ``(batch, dim,
-state_len)`` result, zero padding included.
+state_len)`` result, zero padding included. Like the reference's copy it
+works for any element type: the kernel moves 1-, 2-, 4-, 8- or 16-byte
+elements bit for bit.
 """
 
 from __future__ import annotations
 
 import torch
 
-from causal_conv1d_amd._dtype import _DTYPE_CODE
 from causal_conv1d_amd._native import native_varlen_states
 
 
@@ -29,8 +30,8 @@ def causal_conv1d_varlen_states(x: torch.Tensor, cu_seqlens: torch.Tensor, state
         raise ValueError(f"x shape {tuple(x.shape)}: expected (total_tokens, dim)")
     if cu_seqlens.dim() != 1 or cu_seqlens.shape[0] < 1:
         raise ValueError(f"cu_seqlens shape {tuple(cu_seqlens.shape)}: expected (batch + 1,)")
-    if x.dtype not in _DTYPE_CODE:
-        raise NotImplementedError(f"unsupported dtype {x.dtype}; only fp16/bf16/fp32 are supported")
+    if x.element_size() not in (1, 2, 4, 8, 16):
+        raise NotImplementedError(f"unsupported dtype {x.dtype}: elements of {x.element_size()} bytes")
     if state_len < 0:
         raise ValueError(f"state_len must be >= 0 (got {state_len})")
     _, dim = x.shape

@@ -19,6 +19,38 @@ int esize(int32_t d) { return d == CC1D_DTYPE_FP32 ? 4 : 2; }
 // it touches; refuse problems whose grids would not fit.
 bool grid_fits(int64_t threads) { return threads / 256 + 1 < kMaxBlocks; }
 
+int bwd_typed_entry(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
+    if (p == nullptr || g == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
+    if (p->seq_idx != nullptr &&
+        (p->initial_states != nullptr || p->dfinal_states != nullptr || p->dinitial_states != nullptr))
+        return CC1D_ERR_EXCLUSIVE;
+    if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p->dim == 0) return CC1D_OK;
+    if (g->dweight == nullptr) return CC1D_ERR_NULL_POINTER;
+    if (p->batch == 0 || p->seqlen == 0) {
+        // no positions: the gradients are sums over no terms
+        const int64_t ws[3] = {0, g->dweight_stride[0], g->dweight_stride[1]};
+        int st = launch_zero3(g->dweight, esize(p->dtype), 1, p->dim, p->width, ws, s);
+        if (st == CC1D_OK && g->dbias != nullptr) {
+            const int64_t bs[3] = {0, g->dbias_stride, 0};
+            st = launch_zero3(g->dbias, esize(p->dtype), 1, p->dim, 1, bs, s);
+        }
+        if (st == CC1D_OK && p->dinitial_states != nullptr && p->batch > 0)
+            st = launch_zero3(p->dinitial_states, esize(p->dtype), p->batch, p->dim, p->width - 1,
+                              p->dinitial_states_stride, s);
+        return st;
+    }
+    if (!grid_fits(p->batch * p->dim * p->seqlen)) return CC1D_ERR_SHAPE;
+    if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr)
+        return CC1D_ERR_NULL_POINTER;
+    if (g->workspace == nullptr) return CC1D_ERR_NULL_POINTER;
+    return launch_bwd_typed(*p, *g, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -29,7 +61,7 @@ const char* cc1d_strerror(int status) {
     switch (status) {
     case CC1D_OK: return "ok";
     case CC1D_ERR_NULL_POINTER: return "a required pointer is NULL";
-    case CC1D_ERR_DTYPE: return "unsupported dtype code (expected 0=fp16, 1=bf16, 2=fp32)";
+    case CC1D_ERR_DTYPE: return "unsupported dtype code (expected 0=fp16, 1=bf16, 2=fp32) or element size";
     case CC1D_ERR_WIDTH: return "width must be in 2..9";
     case CC1D_ERR_SHAPE: return "invalid or too large shape";
     case CC1D_ERR_EXCLUSIVE: return "seq_idx is mutually exclusive with initial_states and final_states";
@@ -91,34 +123,7 @@ int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* p) {
 }
 
 int cc1d_bwd_typed(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
-    if (p == nullptr || g == nullptr) return CC1D_ERR_NULL_POINTER;
-    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
-    if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
-    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0) return CC1D_ERR_SHAPE;
-    if (p->seq_idx != nullptr &&
-        (p->initial_states != nullptr || p->dfinal_states != nullptr || p->dinitial_states != nullptr))
-        return CC1D_ERR_EXCLUSIVE;
-    if (p->initial_states != nullptr && p->dinitial_states == nullptr) return CC1D_ERR_NULL_POINTER;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (p->dim == 0) return CC1D_OK;
-    if (g->dweight == nullptr) return CC1D_ERR_NULL_POINTER;
-    if (p->batch == 0 || p->seqlen == 0) {
-        // no positions: the gradients are sums over no terms
-        const int64_t ws[3] = {0, g->dweight_stride[0], g->dweight_stride[1]};
-        int st = launch_zero3(g->dweight, esize(p->dtype), 1, p->dim, p->width, ws, s);
-        if (st == CC1D_OK && g->dbias != nullptr) {
-            const int64_t bs[3] = {0, g->dbias_stride, 0};
-            st = launch_zero3(g->dbias, esize(p->dtype), 1, p->dim, 1, bs, s);
-        }
-        if (st == CC1D_OK && p->dinitial_states != nullptr && p->batch > 0)
-            st = launch_zero3(p->dinitial_states, esize(p->dtype), p->batch, p->dim, p->width - 1,
-                              p->dinitial_states_stride, s);
-        return st;
-    }
-    if (!grid_fits(p->batch * p->dim * p->seqlen)) return CC1D_ERR_SHAPE;
-    if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr || g->workspace == nullptr)
-        return CC1D_ERR_NULL_POINTER;
-    return launch_bwd_typed(*p, *g, s);
+    return bwd_typed_entry(p, g, stream);
 }
 
 int cc1d_update(const cc1d_update_params* p, void* stream) {
@@ -138,7 +143,10 @@ int cc1d_update(const cc1d_update_params* p, void* stream) {
 
 int cc1d_varlen_states(const cc1d_varlen_params* p, void* stream) {
     if (p == nullptr) return CC1D_ERR_NULL_POINTER;
-    if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
+    if (p->elem_bytes == 0 ? !valid_dtype(p->dtype)
+                           : (p->elem_bytes != 1 && p->elem_bytes != 2 && p->elem_bytes != 4 && p->elem_bytes != 8 &&
+                              p->elem_bytes != 16))
+        return CC1D_ERR_DTYPE;
     if (p->total_tokens < 0 || p->dim < 0 || p->batch < 0 || p->state_len < 0) return CC1D_ERR_SHAPE;
     if (p->batch == 0 || p->dim == 0 || p->state_len == 0) return CC1D_OK;
     if (!grid_fits(p->batch * p->dim * p->state_len)) return CC1D_ERR_SHAPE;

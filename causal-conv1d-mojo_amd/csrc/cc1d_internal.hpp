@@ -18,6 +18,8 @@ int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStrea
 int64_t bwd_workspace_floats(const cc1d_bwd_params& p);
 int launch_update(const cc1d_update_params& p, hipStream_t stream);
 int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream);
+// element size of a varlen gather: elem_bytes, or the size of dtype when it is 0
+int varlen_elem_bytes(const cc1d_varlen_params& p);
 
 // Compile-time dispatch over the runtime dtype code / width / flags.
 template <typename F> int with_dtype(int dtype, F&& f) {

@@ -133,17 +133,21 @@ __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
     for (int n = 0; n < W; ++n) wv[n] = vload(wp + n * EPV);
     const u32x4 bv = p.bias ? vload(static_cast<const T*>(p.bias) + c0) : vzero();
 
+    // row[q]: the pool row of entry b0 + q, or -1 for a padding (any
+    // negative) or out-of-pool index; in_batch[q]: the entry exists
     int32_t row[BPL];
+    bool in_batch[BPL];
     u32x4 xv[BPL], sv[BPL][NV];
 #pragma unroll
     for (int q = 0; q < BPL; ++q) {
-        const uint32_t b = b0 + q < nb ? b0 + q : 0;
+        in_batch[q] = b0 + q < nb;
+        const uint32_t b = in_batch[q] ? b0 + q : 0;
         int32_t r = (int32_t)b;
         if (p.conv_state_indices != nullptr) {
             r = UB ? ld_uniform(p.conv_state_indices + b) : p.conv_state_indices[b];
-            if (r >= p.state_rows) r = -1;
+            if (r < 0 || r >= p.state_rows) r = -1;
         }
-        row[q] = (b0 + q < nb) ? r : -2;
+        row[q] = r;
         const uint32_t rr = r >= 0 ? (uint32_t)r : 0u;
         xv[q] = vload(static_cast<const T*>(p.x) + (size_t)b * p.x_stride[0] + c0);
         const T* sp = static_cast<const T*>(p.conv_state) + (size_t)rr * p.conv_state_stride[0] + (size_t)c0 * H;
@@ -174,7 +178,7 @@ __global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
 #pragma unroll
             for (int i = 0; i < H; ++i) ns[e * H + i] = win[i + 1];
         }
-        if (row[q] == -2) continue;  // past the batch
+        if (!in_batch[q]) continue;
         T* op = static_cast<T*>(p.out) + (size_t)(b0 + q) * p.out_stride[0] + c0;
         if (row[q] < 0) {  // padding (or out-of-pool) entry: zero output, state untouched
             vstore(op, vzero());

@@ -3,7 +3,8 @@
 // states[i, c, s] = x[end_i - (S - s), c] when that token belongs to sequence
 // i (cu_seqlens[i] <= token < cu_seqlens[i+1]), else 0 -- the last
 // state_len tokens of each sequence, left zero-padded
-// (src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-61). One thread per
+// (src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-61), for elements of
+// 1, 2, 4, 8 or 16 bytes copied bit for bit. One thread per
 // output element, channels fastest, so both the reads of x (token-major) and
 // the writes of the (batch, state_len, dim)-allocated output are coalesced.
 #include "cc1d_internal.hpp"
@@ -17,8 +18,17 @@ struct VarArgs {
 
 __device__ __forceinline__ int64_t clamp_tok(int64_t v, int64_t n) { return v < 0 ? 0 : (v > n ? n : v); }
 
-template <typename T>
+// Elements are moved as raw bits of their size (E bytes), so any dtype works.
+template <int E> struct Raw;
+template <> struct Raw<1> { typedef uint8_t type; };
+template <> struct Raw<2> { typedef uint16_t type; };
+template <> struct Raw<4> { typedef uint32_t type; };
+template <> struct Raw<8> { typedef uint64_t type; };
+template <> struct Raw<16> { typedef u32x4 type; };
+
+template <int E>
 __global__ void __launch_bounds__(256) varlen_states_kernel(const VarArgs a) {
+    typedef typename Raw<E>::type T;
     const cc1d_varlen_params& p = a.p;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= a.n_items) return;
@@ -36,15 +46,25 @@ __global__ void __launch_bounds__(256) varlen_states_kernel(const VarArgs a) {
     static_cast<T*>(p.states)[i * p.states_stride[0] + c * p.states_stride[1] + s * p.states_stride[2]] = val;
 }
 
+int varlen_elem_bytes(const cc1d_varlen_params& p) {
+    if (p.elem_bytes != 0) return p.elem_bytes;
+    return p.dtype == CC1D_DTYPE_FP32 ? 4 : 2;
+}
+
 int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream) {
-    return with_dtype(p.dtype, [&](auto tag) {
-        using T = decltype(tag);
-        VarArgs a;
-        a.p = p;
-        a.n_items = p.batch * p.state_len * p.dim;
-        varlen_states_kernel<T><<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
-        return launch_status();
-    });
+    VarArgs a;
+    a.p = p;
+    a.n_items = p.batch * p.state_len * p.dim;
+    const dim3 grid((unsigned)ceil_div(a.n_items, 256));
+    switch (varlen_elem_bytes(p)) {
+    case 1: varlen_states_kernel<1><<<grid, 256, 0, stream>>>(a); break;
+    case 2: varlen_states_kernel<2><<<grid, 256, 0, stream>>>(a); break;
+    case 4: varlen_states_kernel<4><<<grid, 256, 0, stream>>>(a); break;
+    case 8: varlen_states_kernel<8><<<grid, 256, 0, stream>>>(a); break;
+    case 16: varlen_states_kernel<16><<<grid, 256, 0, stream>>>(a); break;
+    default: return CC1D_ERR_DTYPE;
+    }
+    return launch_status();
 }
 
 template <typename U>

@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define CC1D_ABI_VERSION 2
+#define CC1D_ABI_VERSION 3
 
 enum cc1d_dtype {
     CC1D_DTYPE_FP16 = 0,
@@ -53,7 +53,7 @@ enum cc1d_dtype {
 enum cc1d_status {
     CC1D_OK = 0,
     CC1D_ERR_NULL_POINTER = 1,      /* a required pointer (or the params struct) is NULL */
-    CC1D_ERR_DTYPE = 2,             /* dtype code not in {0, 1, 2} */
+    CC1D_ERR_DTYPE = 2,             /* dtype code not in {0, 1, 2} (varlen: or elem_bytes not in {0, 1, 2, 4, 8, 16}) */
     CC1D_ERR_WIDTH = 3,             /* width outside 2..9 */
     CC1D_ERR_SHAPE = 4,             /* negative size, or a size/stride too large for the kernels */
     CC1D_ERR_EXCLUSIVE = 5,         /* seq_idx given together with initial_states or final_states
@@ -179,9 +179,13 @@ typedef struct cc1d_update_params {
 /*
  * Varlen state gather: states[i, :, state_len-n+j] = x[start+j, :] for the
  * last n = min(state_len, len_i) tokens of packed sequence i
- * (cu_seqlens[i] .. cu_seqlens[i+1]); all other entries are written 0.
- * cu_seqlens values are clamped to [0, total_tokens].
- * Semantics: src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-61.
+ * (cu_seqlens[i] .. cu_seqlens[i+1]); all other entries are written 0 (all
+ * bits clear). cu_seqlens values are clamped to [0, total_tokens]. It is a
+ * copy, so any element type works: elem_bytes = 1, 2, 4, 8 or 16 moves
+ * elements of that size bit for bit (fp64, integers, bool, complex ...) and
+ * dtype is ignored; elem_bytes = 0 takes the size of dtype.
+ * Semantics: src/causal_conv1d_mojo/causal_conv1d_varlen.py:29-61 (a torch
+ * copy there, so dtype-agnostic).
  */
 typedef struct cc1d_varlen_params {
     const void* x;                 /* (total_tokens, dim) */
@@ -190,8 +194,8 @@ typedef struct cc1d_varlen_params {
     int64_t total_tokens, dim, batch, state_len;
     int64_t x_stride[2];
     int64_t states_stride[3];
-    int32_t dtype;
-    int32_t reserved;
+    int32_t dtype;                 /* enum cc1d_dtype; used only when elem_bytes == 0 */
+    int32_t elem_bytes;            /* 0, or 1 / 2 / 4 / 8 / 16 */
 } cc1d_varlen_params;
 
 int cc1d_abi_version(void);
@@ -211,6 +215,7 @@ int cc1d_bwd(const cc1d_bwd_params* params, void* stream);
  */
 int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* params);
 int cc1d_bwd_typed(const cc1d_bwd_params* params, const cc1d_bwd_grads* grads, void* stream);
+
 int cc1d_update(const cc1d_update_params* params, void* stream);
 int cc1d_varlen_states(const cc1d_varlen_params* params, void* stream);
 

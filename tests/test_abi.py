@@ -50,7 +50,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.cc1d_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.cc1d_abi_version() == _lib.ABI_VERSION == 3
     for code in range(0, 9):
         msg = lib.cc1d_strerror(code).decode()
         assert msg and msg != "unknown status"
@@ -188,6 +188,10 @@ def test_varlen_validation_codes(lib):
 
     assert lib.cc1d_varlen_states(None, None) == ERR_NULL
     assert call(dtype=7) == ERR_DTYPE
+    # an element size overrides the dtype code; only 1, 2, 4, 8 and 16 bytes
+    for e in (3, 5, 32, -1):
+        assert call(elem_bytes=e) == ERR_DTYPE
+    assert call(dtype=7, elem_bytes=8) == ERR_NULL  # valid up to the missing pointers
     assert call(state_len=-1) == ERR_SHAPE
     assert call() == ERR_NULL
     assert call(batch=0) == OK

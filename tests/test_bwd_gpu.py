@@ -22,6 +22,7 @@ from _util import (
     assert_reduction_close,
     grads_f64,
     make_inputs,
+    scales,
     seq_pattern,
 )
 from oracle import oracle as O
@@ -50,15 +51,16 @@ def _gpu_grads(x, w, b, dout, *, init=None, seq_idx=None, activation=None, dfs=N
             None if ig is None else ig.grad.cpu())
 
 
-def _check(got, ref, dtype, has_init=False):
+def _check(got, ref, dtype, scale, has_init=False):
     dx, dw, db, di = got
     rdx, rdw, rdb, rdi = ref
+    sw, sb = scale
     assert dx.dtype == dtype and dw.dtype == dtype
     assert_close(dx, rdx, dtype, name="dx")
-    assert_reduction_close(dw, rdw, dtype, name="dweight")
+    assert_reduction_close(dw, rdw, dtype, scale=sw, name="dweight")
     if rdb is not None:
         assert db.dtype == dtype
-        assert_reduction_close(db, rdb, dtype, name="dbias")
+        assert_reduction_close(db, rdb, dtype, scale=sb, name="dbias")
     if has_init:
         assert_close(di, rdi, dtype, name="dinitial_states")
 
@@ -71,7 +73,8 @@ def test_backward_contiguous(shape, dtype, activation, has_bias):
     x, w, b, _ = make_inputs(*shape, 4, dtype=dtype, has_bias=has_bias)
     dout = make_inputs(*shape, 4, dtype=dtype, seed=1)[0]
     got = _gpu_grads(x, w, b, dout, activation=activation)
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation=activation), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation=activation), dtype,
+           scales(x, w, b, dout, activation=activation))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -83,7 +86,7 @@ def test_backward_width_sweep(dtype, width, seqlen):
     x, w, b, _ = make_inputs(2, 32, seqlen, width, dtype=dtype)
     dout = make_inputs(2, 32, seqlen, width, dtype=dtype, seed=1)[0]
     got = _gpu_grads(x, w, b, dout, activation="silu")
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype, scales(x, w, b, dout, activation="silu"))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -92,7 +95,7 @@ def test_backward_unaligned_and_segmented(dtype, seqlen):
     x, w, b, _ = make_inputs(3, 12, seqlen, 4, dtype=dtype)
     dout = make_inputs(3, 12, seqlen, 4, dtype=dtype, seed=1)[0]
     got = _gpu_grads(x, w, b, dout, activation="silu")
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype, scales(x, w, b, dout, activation="silu"))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -103,7 +106,8 @@ def test_final_states_backward(dtype, width, seqlen):
     dout = make_inputs(2, 16, seqlen, width, dtype=dtype, seed=1)[0]
     dfs = make_inputs(2, 16, width - 1, width, dtype=dtype, seed=2)[0]
     got = _gpu_grads(x, w, b, dout, activation="silu", dfs=dfs)
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, dfinal_states=dfs, activation="silu"), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, dfinal_states=dfs, activation="silu"), dtype,
+           scales(x, w, b, dout, activation="silu"))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -115,7 +119,7 @@ def test_initial_states_backward(dtype, width, seqlen, has_bias):
     dout = make_inputs(2, 16, seqlen, width, dtype=dtype, seed=1)[0]
     got = _gpu_grads(x, w, b, dout, init=init, activation="silu")
     ref = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init, activation="silu")
-    _check(got, ref, dtype, has_init=True)
+    _check(got, ref, dtype, scales(x, w, b, dout, init=init, activation="silu"), has_init=True)
 
 
 @pytest.mark.parametrize("pattern", SEQ_PATTERNS)
@@ -126,7 +130,8 @@ def test_seq_idx_backward(pattern, dtype, activation):
     dout = make_inputs(2, 16, 64, 4, dtype=dtype, seed=1)[0]
     s = seq_pattern(pattern, 2, 64)
     got = _gpu_grads(x, w, b, dout, seq_idx=s, activation=activation)
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation=activation), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation=activation), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation=activation))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -136,7 +141,8 @@ def test_seq_idx_backward_segments(dtype, seqlen):
     dout = make_inputs(2, 8, seqlen, 4, dtype=dtype, seed=1)[0]
     s = seq_pattern("random_runs", 2, seqlen)
     got = _gpu_grads(x, w, b, dout, seq_idx=s, activation="silu")
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation="silu"))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -156,9 +162,10 @@ def test_backward_strided(dtype, layout):
     dout = torch.randn(B, D, L, generator=g).to(dtype)
     dbase, dw, db, _ = _gpu_grads(base, w, b, dout, activation="silu", view=view)
     rdx, rdw, rdb, _ = O.causal_conv1d_bwd(view(base), w, b, dout, activation="silu")
+    sw, sb = scales(view(base), w, b, dout, activation="silu")
     assert_close(view(dbase), rdx, dtype, name="dx")
-    assert_reduction_close(dw, rdw, dtype, name="dweight")
-    assert_reduction_close(db, rdb, dtype, name="dbias")
+    assert_reduction_close(dw, rdw, dtype, scale=sw, name="dweight")
+    assert_reduction_close(db, rdb, dtype, scale=sb, name="dbias")
 
 
 def test_backward_vs_fp64_autograd():
@@ -166,7 +173,8 @@ def test_backward_vs_fp64_autograd():
     x, w, b, init = make_inputs(2, 32, 256, 4, dtype=torch.float32, has_init=True)
     dout = torch.randn(x.shape)
     got = _gpu_grads(x, w, b, dout, init=init, activation="silu")
-    _check(got, grads_f64(x, w, b, dout, init=init, silu=True), torch.float32, has_init=True)
+    _check(got, grads_f64(x, w, b, dout, init=init, silu=True), torch.float32,
+           scales(x, w, b, dout, init=init, activation="silu"), has_init=True)
 
 
 def test_expanded_dout_from_sum():
@@ -175,7 +183,8 @@ def test_expanded_dout_from_sum():
     cc.causal_conv1d_fn(xg, wg, bg, activation="silu").sum().backward()
     rdx, rdw, rdb, _ = O.causal_conv1d_bwd(x, w, b, torch.ones_like(x), activation="silu")
     assert_close(xg.grad.cpu(), rdx, torch.float16)
-    assert_reduction_close(wg.grad.cpu(), rdw, torch.float16)
+    assert_reduction_close(wg.grad.cpu(), rdw, torch.float16,
+                           scale=scales(x, w, b, torch.ones_like(x), activation="silu")[0])
 
 
 @pytest.mark.parametrize("shape", [(0, 64, 128), (2, 0, 128), (2, 64, 0), (0, 0, 0)])
@@ -276,10 +285,11 @@ def test_typed_op_matches_accumulator_op(dtype, layout, case):
     assert layout != "strided" or x.stride(-1) == 2
     acc, typed = _op_both(x, w, b, dout, seq_idx=seq, init=init, dfs=dfs)
     x, dout = x.cpu(), dout.cpu()
+    sw, sb = scales(x, w, b, dout, init=init, seq_idx=seq, activation="silu")
     assert torch.equal(acc[0], typed[0])
-    assert_reduction_close(typed[1], acc[1], dtype, name="dweight")
+    assert_reduction_close(typed[1], acc[1], dtype, scale=sw, name="dweight")
     if b is not None:
-        assert_reduction_close(typed[2], acc[2], dtype, name="dbias")
+        assert_reduction_close(typed[2], acc[2], dtype, scale=sb, name="dbias")
     else:
         assert typed[2] is None
     if init is not None:
@@ -287,4 +297,4 @@ def test_typed_op_matches_accumulator_op(dtype, layout, case):
     ref = O.causal_conv1d_bwd(x.contiguous(), w, b, dout.contiguous(), seq_idx=seq, initial_states=init,
                               dfinal_states=dfs, activation="silu")
     assert_close(typed[0].cpu(), ref[0], dtype, name="dx")
-    assert_reduction_close(typed[1].cpu(), ref[1], dtype, name="dweight")
+    assert_reduction_close(typed[1].cpu(), ref[1], dtype, scale=sw, name="dweight")

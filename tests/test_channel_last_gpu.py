@@ -24,6 +24,7 @@ from _util import (
     assert_equal,
     assert_reduction_close,
     make_inputs,
+    scales,
     seq_pattern,
 )
 from oracle import oracle as O
@@ -98,12 +99,13 @@ def _grads(x, w, b, dout, *, init=None, seq_idx=None, dfs=None, activation="silu
             None if ig is None else ig.grad.cpu())
 
 
-def _check(got, ref, dtype, has_init=False):
+def _check(got, ref, dtype, scale, has_init=False):
     dx, dw, db, di = got
     rdx, rdw, rdb, rdi = ref
+    sw, sb = scale
     assert_close(dx, rdx, dtype, name="dx")
-    assert_reduction_close(dw, rdw, dtype, name="dweight")
-    assert_reduction_close(db, rdb, dtype, name="dbias")
+    assert_reduction_close(dw, rdw, dtype, scale=sw, name="dweight")
+    assert_reduction_close(db, rdb, dtype, scale=sb, name="dbias")
     if has_init:
         assert_close(di, rdi, dtype, name="dinitial_states")
 
@@ -114,7 +116,8 @@ def _check(got, ref, dtype, has_init=False):
 def test_cl_backward(dtype, width, seqlen, dim):
     x, w, b, _ = make_inputs(2, dim, seqlen, width, dtype=dtype)
     dout = make_inputs(2, dim, seqlen, width, dtype=dtype, seed=1)[0]
-    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype)
+    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), dtype,
+           scales(x, w, b, dout, activation="silu"))
 
 
 @pytest.mark.parametrize("pattern", SEQ_PATTERNS)
@@ -125,7 +128,8 @@ def test_cl_backward_seq_idx(pattern, dtype, width, seqlen):
     x, w, b, _ = make_inputs(2, 130, seqlen, width, dtype=dtype)
     dout = make_inputs(2, 130, seqlen, width, dtype=dtype, seed=1)[0]
     s = seq_pattern(pattern, 2, seqlen)
-    _check(_grads(x, w, b, dout, seq_idx=s), O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype)
+    _check(_grads(x, w, b, dout, seq_idx=s), O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation="silu"))
 
 
 @pytest.mark.parametrize("dtype,width", list(_fwd_cases()))
@@ -138,7 +142,8 @@ def test_cl_backward_seq_idx_widths(dtype, width, pattern, activation):
     dout = make_inputs(3, 192, 300, width, dtype=dtype, seed=1)[0]
     s = seq_pattern(pattern, 3, 300)
     got = _grads(x, w, b, dout, seq_idx=s, activation=activation)
-    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation=activation), dtype)
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation=activation), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation=activation))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -150,7 +155,7 @@ def test_cl_backward_states(dtype, width, seqlen):
     dfs = make_inputs(2, 64, width - 1, width, dtype=dtype, seed=2)[0]
     got = _grads(x, w, b, dout, init=init, dfs=dfs)
     ref = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init, dfinal_states=dfs, activation="silu")
-    _check(got, ref, dtype, has_init=True)
+    _check(got, ref, dtype, scales(x, w, b, dout, init=init, activation="silu"), has_init=True)
 
 
 def test_cl_backward_many_tile_groups():
@@ -158,4 +163,5 @@ def test_cl_backward_many_tile_groups():
     channel's accumulators from many blocks."""
     x, w, b, _ = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16)
     dout = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16, seed=1)[0]
-    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), torch.bfloat16)
+    _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), torch.bfloat16,
+           scales(x, w, b, dout, activation="silu"))

@@ -28,7 +28,7 @@ import torch
 import torch.nn.functional as F
 
 import causal_conv1d_amd as cc
-from _util import assert_close, assert_equal, assert_reduction_close
+from _util import assert_close, assert_equal, assert_reduction_close, dpre_f64, taps_f64, weight_grads_from_dpre
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -42,22 +42,7 @@ def _gen(seed):
 
 def _closed_form(x, w, b, seq=None, init=None, silu=False):
     """fp64 forward pieces on the GPU: (pre, out, padded x, tap masks)."""
-    xd = x.double()
-    wd = w.double()
-    B, D, L = x.shape
-    W = w.shape[1]
-    H = W - 1
-    xp = torch.cat([init.double(), xd], -1) if init is not None else F.pad(xd, (H, 0))
-    masks = None
-    if seq is not None:
-        sp = F.pad(seq.long(), (H, 0), value=-(2 ** 40))  # positions before 0 never match
-        masks = [(sp[:, k:k + L] == seq.long()).unsqueeze(1) for k in range(W)]
-    pre = torch.zeros(B, D, L, dtype=torch.float64, device=x.device)
-    if b is not None:
-        pre += b.double()[None, :, None]
-    for k in range(W):
-        term = wd[None, :, k, None] * xp[..., k:k + L]
-        pre += term if masks is None else term * masks[k]
+    pre, xp, masks = taps_f64(x, w, b, seq, init)
     out = F.silu(pre) if silu else pre.clone()
     if seq is not None:
         out = out * (seq >= 0).unsqueeze(1)
@@ -65,19 +50,14 @@ def _closed_form(x, w, b, seq=None, init=None, silu=False):
 
 
 def _closed_form_bwd(x, w, b, dout, seq=None, init=None, silu=False):
-    pre, _, xp, masks = _closed_form(x, w, b, seq, init, silu)
+    """fp64 (dx, dweight, dbias, dinit) on the GPU, plus the magnitude sums
+    (S_dweight, S_dbias) that bound the dweight / dbias comparisons."""
+    dpre, xp, masks = dpre_f64(x, w, b, dout, seq, init, silu)
     L = x.shape[-1]
     W = w.shape[1]
     H = W - 1
-    dpre = dout.double()
-    if silu:
-        s = torch.sigmoid(pre)
-        dpre = dpre * s * (1 + pre * (1 - s))
-    if seq is not None:
-        dpre = dpre * (seq >= 0).unsqueeze(1)
-    dw = torch.stack([(dpre * xp[..., k:k + L] * (1 if masks is None else masks[k])).sum((0, 2))
-                      for k in range(W)], 1)
-    db = dpre.sum((0, 2))
+    dw, db = weight_grads_from_dpre(dpre, xp, masks)
+    sw, sb = weight_grads_from_dpre(dpre, xp, masks, absolute=True)
     # dx[t] = sum_k w[W-1-k] dpre[t+k], gated on seq[t+k] == seq[t]
     dp = F.pad(dpre, (0, H))
     dx = torch.zeros_like(dpre)
@@ -91,7 +71,7 @@ def _closed_form_bwd(x, w, b, dout, seq=None, init=None, silu=False):
     if init is not None:
         dinit = torch.stack([sum(w.double()[None, :, k] * dpre[..., i - k] for k in range(i + 1))
                              for i in range(H)], -1)
-    return dx, dw, db, dinit
+    return dx, dw, db, dinit, sw, sb
 
 
 def _sample_channels(D, n=48, seed=0):
@@ -121,18 +101,18 @@ def test_c2_forward_backward_full_size():
     # every element vs the fp64 closed form
     _, ref_out, _, _ = _closed_form(x.to(DEV), w.to(DEV), b.to(DEV), silu=True)
     assert_close(out.detach(), ref_out, torch.bfloat16, name="out")
-    rdx, rdw, rdb, _ = _closed_form_bwd(x.to(DEV), w.to(DEV), b.to(DEV), dout.to(DEV), silu=True)
+    rdx, rdw, rdb, _, sw, sb = _closed_form_bwd(x.to(DEV), w.to(DEV), b.to(DEV), dout.to(DEV), silu=True)
     assert_close(xg.grad, rdx, torch.bfloat16, name="dx")
-    assert_reduction_close(wg.grad, rdw, torch.bfloat16, name="dweight")
-    assert_reduction_close(bg.grad, rdb, torch.bfloat16, name="dbias")
+    assert_reduction_close(wg.grad, rdw, torch.bfloat16, scale=sw, name="dweight")
+    assert_reduction_close(bg.grad, rdb, torch.bfloat16, scale=sb, name="dbias")
     # sampled channels vs the oracle (identical inputs)
     sel = _sample_channels(D)
     xs, ws, bs, gs = x[:, sel].contiguous(), w[sel].contiguous(), b[sel].contiguous(), dout[:, sel].contiguous()
     assert_close(out.detach().cpu()[:, sel], O.causal_conv1d_fn(xs, ws, bs, activation="silu"), torch.bfloat16)
     odx, odw, odb, _ = O.causal_conv1d_bwd(xs, ws, bs, gs, activation="silu")
     assert_close(xg.grad.cpu()[:, sel], odx, torch.bfloat16, name="dx vs oracle")
-    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, name="dweight vs oracle")
-    assert_reduction_close(bg.grad.cpu()[sel], odb, torch.bfloat16, name="dbias vs oracle")
+    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, scale=sw.cpu()[sel], name="dweight vs oracle")
+    assert_reduction_close(bg.grad.cpu()[sel], odb, torch.bfloat16, scale=sb.cpu()[sel], name="dbias vs oracle")
 
 
 def _c3_inputs():
@@ -163,9 +143,9 @@ def test_c3a_channel_last_varlen_full_size():
     xv = x_store.to(DEV).transpose(1, 2)
     _, ref_out, _, _ = _closed_form(xv, w.to(DEV), None, seq.to(DEV), silu=True)
     assert_close(out.detach(), ref_out, torch.bfloat16, name="out")
-    rdx, rdw, _, _ = _closed_form_bwd(xv, w.to(DEV), None, dout, seq.to(DEV), silu=True)
+    rdx, rdw, _, _, sw, _ = _closed_form_bwd(xv, w.to(DEV), None, dout, seq.to(DEV), silu=True)
     assert_close(xs_g.grad.transpose(1, 2), rdx, torch.bfloat16, name="dx")
-    assert_reduction_close(wg.grad, rdw, torch.bfloat16, name="dweight")
+    assert_reduction_close(wg.grad, rdw, torch.bfloat16, scale=sw, name="dweight")
     sel = _sample_channels(D)
     xcpu = x_store.transpose(1, 2)[:, sel]
     gcpu = dout_store.transpose(1, 2)[:, sel]
@@ -173,7 +153,7 @@ def test_c3a_channel_last_varlen_full_size():
                  torch.bfloat16)
     odx, odw, _, _ = O.causal_conv1d_bwd(xcpu, w[sel], None, gcpu, seq_idx=seq, activation="silu")
     assert_close(xs_g.grad.cpu().transpose(1, 2)[:, sel], odx, torch.bfloat16, name="dx vs oracle")
-    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, name="dweight vs oracle")
+    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, scale=sw.cpu()[sel], name="dweight vs oracle")
 
 
 def test_c3b_channel_last_initial_final_states_full_size():
@@ -189,17 +169,17 @@ def test_c3b_channel_last_initial_final_states_full_size():
     xv = x_store.to(DEV).transpose(1, 2)
     _, ref_out, _, _ = _closed_form(xv, w.to(DEV), None, init=init.to(DEV), silu=True)
     assert_close(out.detach(), ref_out, torch.bfloat16, name="out")
-    rdx, rdw, _, rdi = _closed_form_bwd(xv, w.to(DEV), None, dout_store.to(DEV).transpose(1, 2),
-                                        init=init.to(DEV), silu=True)
+    rdx, rdw, _, rdi, sw, _ = _closed_form_bwd(xv, w.to(DEV), None, dout_store.to(DEV).transpose(1, 2),
+                                               init=init.to(DEV), silu=True)
     assert_close(xs_g.grad.transpose(1, 2), rdx, torch.bfloat16, name="dx")
-    assert_reduction_close(wg.grad, rdw, torch.bfloat16, name="dweight")
+    assert_reduction_close(wg.grad, rdw, torch.bfloat16, scale=sw, name="dweight")
     assert_close(ig.grad, rdi, torch.bfloat16, name="dinitial_states")
     sel = _sample_channels(D)
     odx, odw, _, odi = O.causal_conv1d_bwd(x_store.transpose(1, 2)[:, sel], w[sel], None,
                                            dout_store.transpose(1, 2)[:, sel], initial_states=init[:, sel],
                                            activation="silu")
     assert_close(xs_g.grad.cpu().transpose(1, 2)[:, sel], odx, torch.bfloat16, name="dx vs oracle")
-    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, name="dweight vs oracle")
+    assert_reduction_close(wg.grad.cpu()[sel], odw, torch.bfloat16, scale=sw.cpu()[sel], name="dweight vs oracle")
     assert_close(ig.grad.cpu()[:, sel], odi, torch.bfloat16, name="dinit vs oracle")
 
 
@@ -239,13 +219,13 @@ def test_c5_long_sequence_full_size(dtype, width):
     _, ref_out, _, _ = _closed_form(x, w, None)
     assert_close(out.detach(), ref_out, dtype, name="out")
     del ref_out
-    rdx, rdw, _, _ = _closed_form_bwd(x, w, None, dout)
+    rdx, rdw, _, _, sw, _ = _closed_form_bwd(x, w, None, dout)
     assert_close(xg.grad, rdx, dtype, name="dx")
-    assert_reduction_close(wg.grad, rdw, dtype, name="dweight")
+    assert_reduction_close(wg.grad, rdw, dtype, scale=sw, name="dweight")
     del rdx
     sel = _sample_channels(D, n=16).to(DEV)
     xs, ws, gs = (t.cpu().contiguous() for t in (x[:, sel], w[sel], dout[:, sel]))
     assert_close(out.detach()[:, sel].cpu(), O.causal_conv1d_fn(xs, ws), dtype)
     odx, odw, _, _ = O.causal_conv1d_bwd(xs, ws, None, gs)
     assert_close(xg.grad[:, sel].cpu(), odx, dtype, name="dx vs oracle")
-    assert_reduction_close(wg.grad[sel].cpu(), odw, dtype, name="dweight vs oracle")
+    assert_reduction_close(wg.grad[sel].cpu(), odw, dtype, scale=sw[sel].cpu(), name="dweight vs oracle")

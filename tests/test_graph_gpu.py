@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import causal_conv1d_amd as cc
-from _util import assert_reduction_close, make_inputs
+from _util import assert_reduction_close, make_inputs, scales
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -63,6 +63,7 @@ def test_backward_ops_capture_replay_matches_eager():
     g = _capture(step)
     for i in range(4):
         dout.copy_(torch.randn_like(dout))
+        sw, sb = scales(x, w, b, dout, activation="silu")
         g.replay()
         torch.cuda.synchronize()
         snap = [t.clone() for t in (out, dx, dw, db)]
@@ -72,8 +73,8 @@ def test_backward_ops_capture_replay_matches_eager():
             assert torch.equal(a, e), f"replay {i}: {name}"
         # dweight / dbias gather B fp32 atomic adds per entry in any order: equal up
         # to fp32 rounding (a missing zero-fill on replay would double them)
-        for name, a, e in zip(("dweight", "dbias"), snap[2:], (dw, db)):
-            assert_reduction_close(a, e, torch.float32, name=f"replay {i}: {name}")
+        for name, a, e, sc in zip(("dweight", "dbias"), snap[2:], (dw, db), (sw, sb)):
+            assert_reduction_close(a, e, torch.float32, scale=sc, name=f"replay {i}: {name}")
 
 
 def test_update_capture_replay_matches_eager():
@@ -121,6 +122,7 @@ def test_autograd_backward_capture_replay_is_bit_identical():
     g = _capture(step)
     for i in range(4):
         dout.copy_(torch.randn_like(dout))
+        sw, sb = scales(x, w, b, dout, activation="silu")
         g.replay()
         torch.cuda.synchronize()
         snap = [t.clone() for t in grads]

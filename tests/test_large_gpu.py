@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import causal_conv1d_amd as cc
-from _util import assert_close, assert_reduction_close
+from _util import assert_close, assert_reduction_close, scales
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -59,6 +59,7 @@ def test_channel_last_batch_beyond_2_31_elements():
     dout = torch.randn(B, L, D, generator=g, device=DEV, dtype=torch.bfloat16).transpose(1, 2)
     (dw,) = torch.autograd.grad(out, (wg,), dout)
     _, rdw, _, _ = O.causal_conv1d_bwd(xs, ws, None, _sample(dout, chans), activation="silu")
-    assert_reduction_close(dw[chans].cpu(), rdw, torch.bfloat16, name="dweight")
+    sw, _ = scales(xs, ws, None, _sample(dout, chans), activation="silu")
+    assert_reduction_close(dw[chans].cpu(), rdw, torch.bfloat16, scale=sw, name="dweight")
     del base, x, out, dout
     torch.cuda.empty_cache()

@@ -29,6 +29,9 @@ from _util import (
     final_states_expected,
     grads_f64,
     make_inputs,
+    reduction_bound,
+    reduction_scale,
+    scales,
     seq_pattern,
 )
 from oracle import oracle as O
@@ -170,9 +173,10 @@ def test_golden_backward_with_initial_and_final_states():
         z["x"], z["weight"], z["bias"], z["dout"], initial_states=z["initial_states"],
         dfinal_states=z["dfinal_states"], activation="silu",
     )
+    sw, sb = scales(z["x"], z["weight"], z["bias"], z["dout"], init=z["initial_states"], activation="silu")
     assert_close(dx, z["dx"], torch.float32, name="dx")
-    assert_reduction_close(dw, z["dweight"], torch.float32, name="dweight")
-    assert_reduction_close(db, z["dbias"], torch.float32, name="dbias")
+    assert_reduction_close(dw, z["dweight"], torch.float32, scale=sw, name="dweight")
+    assert_reduction_close(db, z["dbias"], torch.float32, scale=sb, name="dbias")
     assert_close(dinit, z["dinitial_states"], torch.float32, name="dinit")
 
 
@@ -180,9 +184,10 @@ def test_golden_backward_seq_idx():
     z = _load("seq_repeat_fp32.npz")
     dx, dw, db, _ = O.causal_conv1d_bwd(z["x"], z["weight"], z["bias"], z["dout"], seq_idx=z["seq_idx"],
                                         activation="silu")
+    sw, sb = scales(z["x"], z["weight"], z["bias"], z["dout"], seq_idx=z["seq_idx"], activation="silu")
     assert_close(dx, z["dx"], torch.float32, name="dx")
-    assert_reduction_close(dw, z["dweight"], torch.float32, name="dweight")
-    assert_reduction_close(db, z["dbias"], torch.float32, name="dbias")
+    assert_reduction_close(dw, z["dweight"], torch.float32, scale=sw, name="dweight")
+    assert_reduction_close(db, z["dbias"], torch.float32, scale=sb, name="dbias")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
@@ -195,9 +200,10 @@ def test_backward_matches_autograd_f64(dtype, width, silu, has_init):
     dx, dw, db, dinit = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init,
                                             activation="silu" if silu else None)
     rdx, rdw, rdb, rdinit = grads_f64(x, w, b, dout, init=init, silu=silu)
+    sw, sb = reduction_scale(x, w, b, dout, init=init, silu=silu)
     assert_close(dx, rdx, dtype, name="dx")
-    assert_reduction_close(dw, rdw, dtype, name="dweight")
-    assert_reduction_close(db, rdb, dtype, name="dbias")
+    assert_reduction_close(dw, rdw, dtype, scale=sw, name="dweight")
+    assert_reduction_close(db, rdb, dtype, scale=sb, name="dbias")
     if has_init:
         assert_close(dinit, rdinit, dtype, name="dinit")
 
@@ -209,9 +215,10 @@ def test_backward_seq_idx_matches_autograd_f64(pattern):
     s = seq_pattern(pattern, 2, 64)
     dx, dw, db, _ = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu")
     rdx, rdw, rdb, _ = grads_f64(x, w, b, dout, seq_idx=s, silu=True)
+    sw, sb = reduction_scale(x, w, b, dout, seq_idx=s, silu=True)
     assert_close(dx, rdx, torch.float32, name="dx")
-    assert_reduction_close(dw, rdw, torch.float32, name="dweight")
-    assert_reduction_close(db, rdb, torch.float32, name="dbias")
+    assert_reduction_close(dw, rdw, torch.float32, scale=sw, name="dweight")
+    assert_reduction_close(db, rdb, torch.float32, scale=sb, name="dbias")
 
 
 def test_backward_planted_missing_silu_grad_is_caught():
@@ -221,6 +228,87 @@ def test_backward_planted_missing_silu_grad_is_caught():
     rdx, _, _, _ = grads_f64(x, w, b, dout, silu=True)
     with pytest.raises(AssertionError):
         assert_close(dx, rdx, torch.float32)
+
+
+def _scale_brute_force(x, w, b, dout, init=None, seq_idx=None, silu=False):
+    """Magnitude sums by explicit loops in float64 (tiny shapes only): per term
+    |dout| * (s (1 + |p| (1 - s)) + |b| + sum_k |w_k xx_k|) * |xx| with SiLU."""
+    B, D, L = x.shape
+    W = w.shape[1]
+    xd, wd, gd = x.double(), w.double(), dout.double()
+    sw = torch.zeros(D, W, dtype=torch.float64)
+    sb = torch.zeros(D, dtype=torch.float64)
+
+    def xx(bi, c, s):
+        if s >= 0:
+            return xd[bi, c, s].item()
+        return init.double()[bi, c, s + W - 1].item() if init is not None else 0.0
+
+    def keep(bi, s, t):
+        return seq_idx is None or (s >= 0 and int(seq_idx[bi, s]) == int(seq_idx[bi, t]))
+
+    for bi in range(B):
+        for c in range(D):
+            for t in range(L):
+                if seq_idx is not None and int(seq_idx[bi, t]) < 0:
+                    continue
+                kept = [k for k in range(W) if keep(bi, t + k - (W - 1), t)]
+                bias = b.double()[c].item() if b is not None else 0.0
+                pre = bias + sum(wd[c, k].item() * xx(bi, c, t + k - (W - 1)) for k in kept)
+                d = abs(gd[bi, c, t].item())
+                if silu:
+                    sg = 1.0 / (1.0 + np.exp(-pre))
+                    pmag = abs(bias) + sum(abs(wd[c, k].item() * xx(bi, c, t + k - (W - 1))) for k in kept)
+                    d *= sg * (1 + abs(pre) * (1 - sg)) + pmag
+                sb[c] += d
+                for k in kept:
+                    sw[c, k] += d * abs(xx(bi, c, t + k - (W - 1)))
+    return sw, sb
+
+
+@pytest.mark.parametrize("case", ["plain", "init", "seq"])
+def test_reduction_scale_matches_brute_force(case):
+    """The per-element bound's magnitude sums, pinned by explicit loops."""
+    x, w, b, init = make_inputs(2, 3, 11, 4, dtype=torch.float32, has_init=case == "init")
+    dout = make_inputs(2, 3, 11, 4, dtype=torch.float32, seed=1)[0]
+    s = torch.tensor([[0, 0, 1, 1, 1, -1, 2, 2, 1, 1, 1]] * 2, dtype=torch.int32) if case == "seq" else None
+    sw, sb = reduction_scale(x, w, b, dout, init=init, seq_idx=s, silu=True)
+    bw, bb = _scale_brute_force(x, w, b, dout, init=init, seq_idx=s, silu=True)
+    assert torch.allclose(sw, bw, rtol=1e-12, atol=0) and torch.allclose(sb, bb, rtol=1e-12, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("plant", ["dropped_tap", "misgated_tap"])
+def test_reduction_bound_catches_error_on_low_magnitude_channel(dtype, plant):
+    """A mistake on one low-magnitude channel fails the per-(channel, tap) bound, while the
+    tensor-wide bound tol * (1 + max|ref|) of the reference's helper would accept it."""
+    B, D, L, W = 2, 16, 256, 4
+    x, w, b, _ = make_inputs(B, D, L, W, dtype=dtype)
+    dout = make_inputs(B, D, L, W, dtype=dtype, seed=1)[0]
+    # channel 5: gradients 1e3 (bf16) / 1e6 (fp32) times smaller than the rest
+    dout[:, 5] = (dout[:, 5].float() * (1e-3 if dtype == torch.bfloat16 else 1e-6)).to(dtype)
+    s = seq_pattern("random_runs", B, L) if plant == "misgated_tap" else None
+    _, dw, db, _ = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu")
+    sw, sb = reduction_scale(x, w, b, dout, seq_idx=s, silu=True)
+    _, rdw, _, _ = grads_f64(x, w, b, dout, seq_idx=s, silu=True)
+    assert_reduction_close(dw, rdw, dtype, scale=sw)  # the unplanted oracle passes
+    planted = dw.double().clone()
+    if plant == "dropped_tap":
+        # tap 0 of channel 5 loses its contribution from batch 1
+        drop = grads_f64(x[1:], w, b, dout[1:], silu=True)[1][5, 0]
+        planted[5, 0] -= drop
+    else:
+        # tap 0 of channel 5 ignores the seq_idx gate at the 7 boundaries of batch 0
+        _, ungated, _, _ = grads_f64(x[:1], w, b, dout[:1], silu=True)
+        _, gated, _, _ = grads_f64(x[:1], w, b, dout[:1], seq_idx=s[:1], silu=True)
+        planted[5, 0] += ungated[5, 0] - gated[5, 0]
+    assert (planted - rdw).abs().max() <= TOL_WIDE[dtype] * (1 + rdw.abs().max())  # the old bound misses it
+    assert ((planted - rdw).abs() > reduction_bound(rdw, sw, dtype)).any()
+    with pytest.raises(AssertionError):
+        assert_reduction_close(planted, rdw, dtype, scale=sw)
+
+
+TOL_WIDE = {torch.float32: 1e-5, torch.bfloat16: 1e-2}
 
 
 # ---------------------------------------------------------------- update

@@ -23,7 +23,7 @@ import pytest
 import torch
 
 import causal_conv1d_amd as cc
-from _util import assert_close, assert_equal, assert_reduction_close
+from _util import assert_close, assert_equal, assert_reduction_close, scales
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -138,9 +138,10 @@ def test_random_forward_backward(c):
     rdx, rdw, rdb, rdi = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=seq, initial_states=init,
                                              dfinal_states=dfs, activation=c["act"])
     assert_close(view(base.grad).cpu(), rdx, dtype, name="dx")
-    assert_reduction_close(wg.grad.t().cpu() if c["wt"] else wg.grad.cpu(), rdw, dtype, name="dweight")
+    sw, sb = scales(x, w, b, dout, init=init, seq_idx=seq, activation=c["act"])
+    assert_reduction_close(wg.grad.t().cpu() if c["wt"] else wg.grad.cpu(), rdw, dtype, scale=sw, name="dweight")
     if b is not None:
-        assert_reduction_close(bg.grad.cpu(), rdb, dtype, name="dbias")
+        assert_reduction_close(bg.grad.cpu(), rdb, dtype, scale=sb, name="dbias")
     if init is not None:
         assert_close(ig.grad.cpu(), rdi, dtype, name="dinitial_states")
 

@@ -5,7 +5,7 @@ state; both the outputs and the mutated conv_state are compared.
 Coverage follows the reference's tests/test_update.py: single token with
 state_len = W-1, short bursts, decode loop == full forward (bit-exact for
 fp16/bf16), circular buffer incl. cache_seqlens >= state_len, circular decode
-loop, conv_state_indices pools, padding (-1) rows, plus the benchmark decode
+loop, conv_state_indices pools, padding rows (-1, -2, INT32_MIN, out of pool), plus the benchmark decode
 shapes at reduced batch and out-of-pool indices.
 """
 
@@ -16,6 +16,7 @@ import torch
 
 import causal_conv1d_amd as cc
 from _util import DTYPE_IDS, DTYPES, assert_close, assert_equal, make_inputs
+from causal_conv1d_amd._native import native_update
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -156,22 +157,40 @@ def test_conv_state_indices_pool(dtype, circular, dim):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("dim", [8, 64, 1024])  # 1024: whole wavefronts per batch entry (scalar index reads)
-def test_padding_and_out_of_pool_rows(dtype, dim):
-    x, w, b, _ = make_inputs(4, dim, 1, 4, dtype=dtype)
-    pool = make_inputs(4, dim, 3, 4, dtype=dtype, seed=1)[0]
-    idx = torch.tensor([0, -1, 2, 4], dtype=torch.int32)  # 4 is outside a pool of 4 rows
+@pytest.mark.parametrize("circular", [False, True])
+def test_padding_and_out_of_pool_rows(dtype, dim, circular):
+    # every negative index is padding (-1, -2, INT32_MIN), and so is an index >= the pool size
+    idx = torch.tensor([0, -1, 2, 4, -2, -(2 ** 31), 3, 9], dtype=torch.int32)
+    B = idx.numel()
+    x, w, b, _ = make_inputs(B, dim, 1, 4, dtype=dtype)
+    S = 16 if circular else 3  # 16: whole 16-byte chunks per state line (the chunked circular kernel)
+    pool = make_inputs(4, dim, S, 4, dtype=dtype, seed=1)[0]
+    cs = torch.tensor([1, 5, 6, 0, 2, 3, 19, 4], dtype=torch.int32) if circular else None
     sg = pool.to(DEV)
-    out = cc.causal_conv1d_update(x[..., 0].to(DEV), sg, w.to(DEV), b.to(DEV), activation="silu",
-                                  conv_state_indices=idx.to(DEV)).cpu()
-    assert torch.all(out[1] == 0) and torch.all(out[3] == 0)
+    # through the C ABI with an output prefilled with NaN, so a padding entry that is not written shows
+    og = torch.full((B, dim, 1), float("nan"), dtype=dtype, device=DEV)
+    native_update(x.to(DEV), w.to(DEV), b.to(DEV), sg, idx.to(DEV), None if cs is None else cs.to(DEV), og, True)
+    out = og[..., 0].cpu()
+    pad = torch.tensor([1, 3, 4, 5, 7])
+    assert torch.all(out[pad] == 0)
     st = sg.cpu()
     assert_equal(st[1], pool[1])
-    assert_equal(st[3], pool[3])
-    real = torch.tensor([0, 2])
+    real = torch.tensor([0, 2, 6])
     rs = pool[idx[real].long()].clone()
-    rout = O.causal_conv1d_update(x[real, :, 0], rs, w, b, activation="silu")
+    kw = dict(activation="silu")
+    if circular:
+        kw["cache_seqlens"] = cs[real]
+    rout = O.causal_conv1d_update(x[real, :, 0], rs, w, b, **kw)
     assert_close(out[real], rout, dtype)
     assert_equal(st[idx[real].long()], rs)
+    # the public API gives the same
+    sg2 = pool.to(DEV)
+    kw2 = dict(activation="silu", conv_state_indices=idx.to(DEV))
+    if circular:
+        kw2["cache_seqlens"] = cs.to(DEV)
+    out2 = cc.causal_conv1d_update(x[..., 0].to(DEV), sg2, w.to(DEV), b.to(DEV), **kw2).cpu()
+    assert_equal(out2, out)
+    assert_equal(sg2.cpu(), st)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])

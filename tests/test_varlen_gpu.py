@@ -53,6 +53,27 @@ def test_random_packing_matches_oracle_and_layout(dtype):
     assert_equal(out.cpu(), O.varlen_states(x, cu, 10))
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.int64, torch.int32, torch.int16, torch.int8, torch.uint8,
+                                   torch.bool, torch.complex64, torch.complex128],
+                         ids=lambda d: str(d).replace("torch.", ""))
+def test_any_element_type_is_copied_bit_for_bit(dtype):
+    """The reference's version is a torch copy, so it accepts every dtype
+    (causal_conv1d_varlen.py:49-60); the gather moves raw 1/2/4/8/16-byte elements."""
+    g = torch.Generator().manual_seed(2)
+    cu = torch.tensor([0, 3, 3, 11, 12, 40], dtype=torch.int32)
+    if dtype.is_complex:
+        x = torch.randn(40, 24, generator=g, dtype=dtype)
+    elif dtype == torch.bool:
+        x = torch.randint(0, 2, (40, 24), generator=g).bool()
+    elif dtype.is_floating_point:
+        x = torch.randn(40, 24, generator=g, dtype=dtype)
+    else:
+        x = torch.randint(-100 if dtype != torch.uint8 else 0, 100, (40, 24), generator=g).to(dtype)
+    out = cc.causal_conv1d_varlen_states(x.to(DEV), cu.to(DEV), 5)
+    assert out.dtype == dtype and out.stride() == (5 * 24, 1, 24)
+    assert torch.equal(out.cpu(), O.varlen_states(x, cu, 5))
+
+
 def test_ref_alias():
     assert cc.causal_conv1d_varlen_states is cc.causal_conv1d_varlen_states_ref
 
