@@ -15,6 +15,8 @@ from pathlib import Path
 
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
 ABI_VERSION = 3
+# fp32 elements of the static device scratch of cc1d_bwd_typed_noalloc (CC1D_NOALLOC_WORKSPACE_FLOATS)
+NOALLOC_WORKSPACE_FLOATS = 1 << 22
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -84,6 +86,7 @@ EXPORTED_SYMBOLS = (
     "cc1d_bwd",
     "cc1d_bwd_workspace_floats",
     "cc1d_bwd_typed",
+    "cc1d_bwd_typed_noalloc",
     "cc1d_update",
     "cc1d_varlen_states",
 )
@@ -118,8 +121,10 @@ def load():
         fn.argtypes = [ctypes.POINTER(st), _vp]
     lib.cc1d_bwd_workspace_floats.restype = ctypes.c_int64
     lib.cc1d_bwd_workspace_floats.argtypes = [ctypes.POINTER(BwdParams)]
-    lib.cc1d_bwd_typed.restype = ctypes.c_int
-    lib.cc1d_bwd_typed.argtypes = [ctypes.POINTER(BwdParams), ctypes.POINTER(BwdGrads), _vp]
+    for name in ("cc1d_bwd_typed", "cc1d_bwd_typed_noalloc"):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(BwdParams), ctypes.POINTER(BwdGrads), _vp]
     got = lib.cc1d_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"causal_conv1d_amd: ABI version mismatch (library {got}, bindings {ABI_VERSION})")

@@ -118,6 +118,20 @@ def native_bwd_typed(x, weight, bias, dout, seq_idx, initial_states, dx, dweight
     _lib.check(lib.cc1d_bwd_typed(ctypes.byref(p), ctypes.byref(g), _stream(x)))
 
 
+def native_bwd_typed_noalloc(x, weight, bias, dout, seq_idx, initial_states, dx, dweight, dbias, dinitial_states,
+                             apply_silu, dfinal_states=None) -> None:
+    """cc1d_bwd_typed_noalloc: as native_bwd_typed, with the library's static device scratch
+    as the workspace (no allocation at all; calls that overlap on one GPU race)."""
+    _require_device(x)
+    lib = _lib.load()
+    p = _bwd_params(x, weight, bias, dout, seq_idx, initial_states, dx, dinitial_states, apply_silu, dfinal_states)
+    g = _lib.BwdGrads()
+    g.dweight, g.dbias = dweight.data_ptr(), _ptr(dbias)
+    _set2(g.dweight_stride, dweight)
+    g.dbias_stride = dbias.stride(0) if dbias is not None else 0
+    _lib.check(lib.cc1d_bwd_typed_noalloc(ctypes.byref(p), ctypes.byref(g), _stream(x)))
+
+
 def native_update(x, weight, bias, conv_state, conv_state_indices, cache_seqlens, out, apply_silu) -> None:
     _require_device(x)
     lib = _lib.load()

@@ -19,7 +19,8 @@ int esize(int32_t d) { return d == CC1D_DTYPE_FP32 ? 4 : 2; }
 // it touches; refuse problems whose grids would not fit.
 bool grid_fits(int64_t threads) { return threads / 256 + 1 < kMaxBlocks; }
 
-int bwd_typed_entry(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
+// Shared by cc1d_bwd_typed and cc1d_bwd_typed_noalloc (which ignores the workspace).
+int bwd_typed_entry(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream, bool noalloc) {
     if (p == nullptr || g == nullptr) return CC1D_ERR_NULL_POINTER;
     if (!valid_dtype(p->dtype)) return CC1D_ERR_DTYPE;
     if (!valid_width(p->width)) return CC1D_ERR_WIDTH;
@@ -47,6 +48,7 @@ int bwd_typed_entry(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* str
     if (!grid_fits(p->batch * p->dim * p->seqlen)) return CC1D_ERR_SHAPE;
     if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr)
         return CC1D_ERR_NULL_POINTER;
+    if (noalloc) return launch_bwd_typed_noalloc(*p, *g, s);
     if (g->workspace == nullptr) return CC1D_ERR_NULL_POINTER;
     return launch_bwd_typed(*p, *g, s);
 }
@@ -68,6 +70,9 @@ const char* cc1d_strerror(int status) {
     case CC1D_ERR_STATE_LEN: return "conv_state length must be >= width - 1";
     case CC1D_ERR_LAUNCH: return "kernel launch failed";
     case CC1D_ERR_WORKSPACE: return "workspace smaller than cc1d_bwd_workspace_floats()";
+    case CC1D_ERR_SCRATCH_LIMIT:
+        return "problem needs more workspace than the static scratch of cc1d_bwd_typed_noalloc "
+               "(CC1D_NOALLOC_WORKSPACE_FLOATS floats)";
     default: return "unknown status";
     }
 }
@@ -123,7 +128,11 @@ int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* p) {
 }
 
 int cc1d_bwd_typed(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
-    return bwd_typed_entry(p, g, stream);
+    return bwd_typed_entry(p, g, stream, false);
+}
+
+int cc1d_bwd_typed_noalloc(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* stream) {
+    return bwd_typed_entry(p, g, stream, true);
 }
 
 int cc1d_update(const cc1d_update_params* p, void* stream) {

@@ -15,6 +15,11 @@ namespace cc1d {
 int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream);
 int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream);
 int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream);
+// As launch_bwd_typed with the library's static device scratch as the
+// workspace (g.workspace is ignored); CC1D_ERR_SCRATCH_LIMIT when the
+// problem needs more than kStaticWorkspaceFloats.
+int launch_bwd_typed_noalloc(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream);
+constexpr int64_t kStaticWorkspaceFloats = CC1D_NOALLOC_WORKSPACE_FLOATS;
 int64_t bwd_workspace_floats(const cc1d_bwd_params& p);
 int launch_update(const cc1d_update_params& p, hipStream_t stream);
 int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream);

@@ -60,8 +60,13 @@ enum cc1d_status {
                                        (backward: or with dfinal_states / dinitial_states) */
     CC1D_ERR_STATE_LEN = 6,         /* conv_state length < width - 1 */
     CC1D_ERR_LAUNCH = 7,            /* the HIP runtime refused a kernel launch */
-    CC1D_ERR_WORKSPACE = 8          /* workspace smaller than cc1d_bwd_workspace_floats() */
+    CC1D_ERR_WORKSPACE = 8,         /* workspace smaller than cc1d_bwd_workspace_floats() */
+    CC1D_ERR_SCRATCH_LIMIT = 9      /* cc1d_bwd_typed_noalloc: the problem needs more than
+                                       CC1D_NOALLOC_WORKSPACE_FLOATS floats of workspace */
 };
+
+/* Size (fp32 elements) of the static device scratch of cc1d_bwd_typed_noalloc: 16 MiB per GPU. */
+#define CC1D_NOALLOC_WORKSPACE_FLOATS ((int64_t)1 << 22)
 
 /*
  * Forward: out[b,c,t] = act(bias[c] + sum_k weight[c,k] * xx(b,c,t+k-(W-1)))
@@ -216,6 +221,23 @@ int cc1d_bwd(const cc1d_bwd_params* params, void* stream);
 int64_t cc1d_bwd_workspace_floats(const cc1d_bwd_params* params);
 int cc1d_bwd_typed(const cc1d_bwd_params* params, const cc1d_bwd_grads* grads, void* stream);
 
+/*
+ * cc1d_bwd_typed without a caller-provided workspace. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The
+ * fp32 partial sums go to a static device array of
+ * CC1D_NOALLOC_WORKSPACE_FLOATS floats inside the library (one per GPU,
+ * held until the process ends); grads->workspace and
+ * grads->workspace_floats are ignored. A problem whose
+ * cc1d_bwd_workspace_floats() exceeds that size returns
+ * CC1D_ERR_SCRATCH_LIMIT and enqueues nothing. The call allocates nothing;
+ * its first call on a device looks up that device's copy of the array
+ * (hipGetSymbolAddress), so make that first call outside graph capture.
+ * Every call on one GPU shares the array: calls that overlap on one GPU (on
+ * other streams or threads) race; calls ordered on one stream do not. The
+ * results are those of cc1d_bwd_typed, bit for bit.
+ */
+int cc1d_bwd_typed_noalloc(const cc1d_bwd_params* params, const cc1d_bwd_grads* grads, void* stream);
 int cc1d_update(const cc1d_update_params* params, void* stream);
 int cc1d_varlen_states(const cc1d_varlen_params* params, void* stream);
 
