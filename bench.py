@@ -11,30 +11,42 @@ Reported (one JSON line):
   value        step throughput in GB/s = algorithmic bytes of the forward and
                backward kernels (167,823,360 + 251,811,840 B) / step time
   roofline     for the dominant kernel (the fused backward): algorithmic bytes
-               per launch / average launch duration, measured here with HIP
+               per launch / median launch duration, measured here with HIP
                events around a graph of back-to-back launches, vs 8 TB/s.
                `traffic` (HBM bytes per launch) is read from the rocprofv3
                --pmc summary committed in profiles/ when present.
-  kernels      the same measurement for the forward kernel and for the decode
-               update (C4a: 256 x 5120 bf16, pool 512 x 5120 x 3, random rows),
-               in GB/s and microseconds per call.
+  kernels      every kernel at every benchmark configuration: median, min and
+               max microseconds per launch over --runs timed graph replays
+               (spread = (max - min) / min), algorithmic GB/s and fraction of
+               8 TB/s at the median. C2 forward / backward / autograd
+               backward; C3a / C3b channel-last (seq_idx / states) forward,
+               backward and autograd backward; C5 (8, 2048, 16384) for fp32,
+               fp16 and bf16 at widths 2, 3, 4; the decode updates C4a and C4b
+               with the bandwidth floors of their access patterns beside them
+               (a plain copy of the same bytes, the same scattered rows or
+               state-line chunks without arithmetic); the varlen state gather.
   cpu_baseline the CPU oracle (C restatement of the reference's CPU kernels,
-               OpenMP) on a bounded sample of C2, on this host.
+               OpenMP) on a bounded sample of C2, on this host; beside it the
+               reference's pure-PyTorch baseline (F.conv1d + F.silu, autograd)
+               on the same sample.
 
-Input sets are rotated so that the data touched between two reuses of a
-buffer exceeds the 256 MB Infinity Cache: every launch streams from HBM.
+Input sets rotate so that the bytes a kernel touches between two reuses of a
+buffer set exceed the 256 MB Infinity Cache, so every launch streams from HBM:
+C2 4 sets (>= 504 MB between reuses), C3 4 sets (>= 403 MB), C4a 42 sets
+(>= 537 MB), C4b 5 sets (>= 671 MB of whole state lines), C5 one set of 1-3 GB.
 
-Modes: --mode bench (default), --mode kernels (eager launch loop of the C2
-forward / backward / C4a update, plus the C3 / C5 / C4b / varlen-states
-launches unless --no-configs, for rocprofv3 --kernel-trace / --pmc), --mode copy (a plain
-1 GiB device copy, the calibration kernel for FETCH_SIZE / WRITE_SIZE).
+Modes: --mode bench (default), --mode kernels (eager launch loop of every
+kernel and floor above, for rocprofv3 --kernel-trace / --pmc; --no-configs
+keeps only C2 and C4a), --mode copy (a plain 1 GiB device copy, the
+calibration kernel for FETCH_SIZE / WRITE_SIZE).
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
-import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -45,13 +57,21 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "fwd/bwd achieved HBM GB/s (% peak) at B4×D5120×L2048 bf16; update µs/call"
 HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 * 2 ** 20
 B, D, L, W = 4, 5120, 2048, 4
 # algorithmic bytes: every input read once, every output written once
 FWD_BYTES = 2 * B * D * L * 2 + D * W * 2 + D * 2                      # 167,823,360
 BWD_BYTES = 3 * B * D * L * 2 + D * W * 2 + D * 2 + D * W * 4 + D * 4  # 251,811,840
+# autograd backward: the same kernel, dweight / dbias written once in bf16 by the reduction
+BWD_TYPED_BYTES = 3 * B * D * L * 2 + D * W * 2 + D * 2 + D * W * 2 + D * 2
 UPD_B, UPD_POOL = 256, 512
 UPD_BYTES = UPD_B * D * (2 + 6 + 6 + 2) + D * W * 2 + D * 2 + UPD_B * 4  # 21,023,744
-MALL_BYTES = 256 * 2 ** 20
+UPD_TOUCHED = UPD_B * D * (2 + 6 + 2)  # distinct bytes a call touches: x, its state rows, out
+C4B_S = 64
+C4B_BYTES = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4  # 39,374,848
+C4B_LINE_BYTES = UPD_B * D * 128  # whole 128-byte state lines under the touched chunks
+
+FLOOR_LIB = ROOT / "causal-conv1d-mojo_amd" / "causal_conv1d_amd" / "_lib" / "libcc1d_floor.so"
 
 
 def log(msg):
@@ -65,25 +85,16 @@ def _parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--mode", choices=["bench", "kernels", "copy"], default="bench")
     ap.add_argument("--launches", type=int, default=40, help="launches per kernel timing graph")
+    ap.add_argument("--runs", type=int, default=5, help="timed graph replays per kernel (min / median / max)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the C3/C4b/C5/varlen report lines")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline duration")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of each CPU-baseline leg")
     ap.add_argument("--settle", type=float, default=0.3,
                     help="seconds of untimed C2 kernels before the first timing (clock ramp)")
     return ap.parse_args()
 
 
-def _c2_sets(torch, n):
-    sets = []
-    for i in range(n):
-        g = torch.Generator(device="cuda").manual_seed(100 + i)
-        x = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
-        dout = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
-        sets.append((x, dout))
-    g = torch.Generator(device="cuda").manual_seed(0)
-    w = torch.randn(D, W, generator=g, device="cuda").bfloat16()
-    b = torch.randn(D, generator=g, device="cuda").bfloat16()
-    return sets, w, b
+# ------------------------------------------------------------------ timing helpers
 
 
 def _graph(torch, fn):
@@ -100,29 +111,113 @@ def _graph(torch, fn):
     return g
 
 
-def _time_graph(torch, g, reps):
-    """Average ms per replay over `reps` replays, HIP events on torch's current stream."""
+def _replay_times(torch, g, runs):
+    """Milliseconds of each of `runs` replays of g (HIP events on torch's current stream,
+    which is where graph replays run), after one untimed replay."""
     g.replay()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for _ in range(reps):
+    out = []
+    for _ in range(runs):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
         g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / reps
+        t1.record()
+        torch.cuda.synchronize()
+        out.append(t0.elapsed_time(t1))
+    return out
 
 
-def _pmc_traffic(kernel):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, or None."""
+def _time_launch_set(torch, fns, launches, runs):
+    """Microseconds per launch, one value per run, of a graph of `launches` launches
+    cycling through the closures `fns` (one per rotating buffer set)."""
+    def loop():
+        for i in range(launches):
+            fns[i % len(fns)]()
+    g = _graph(torch, loop)
+    us = [ms * 1e3 / launches for ms in _replay_times(torch, g, runs)]
+    del g
+    return us
+
+
+def _entry(us_runs, nbytes, **extra):
+    """Report fields of one kernel: median / min / max us per launch over the runs,
+    spread, algorithmic GB/s and fraction of 8 TB/s at the median."""
+    med = statistics.median(us_runs)
+    mn, mx = min(us_runs), max(us_runs)
+    gbps = nbytes / (med * 1e-6) / 1e9
+    return {"us_per_launch": round(med, 2), "us_min": round(mn, 2), "us_max": round(mx, 2),
+            "spread_pct": round((mx - mn) / mn * 100.0, 2), "runs": len(us_runs),
+            "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+            **extra}
+
+
+def _pmc(kernel, key="hbm_bytes_per_launch"):
+    """A field of the committed rocprofv3 --pmc summary (profiles/pmc_summary.json), or None."""
     p = ROOT / "profiles" / "pmc_summary.json"
     if not p.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(kernel, {}).get("hbm_bytes_per_launch")
+        return json.loads(p.read_text()).get(kernel, {}).get(key)
     except (ValueError, OSError):
         return None
+
+
+class Floors:
+    """ctypes binding of the bench's floor kernels (csrc/bench/cc1d_floor.hip)."""
+
+    def __init__(self):
+        if not FLOOR_LIB.exists():
+            raise RuntimeError(f"{FLOOR_LIB} is not built; run `python causal-conv1d-mojo_amd/csrc/build.py`")
+        lib = ctypes.CDLL(str(FLOOR_LIB))
+        i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+        lib.cc1d_floor_copy.argtypes = [vp, vp, i64, vp]
+        lib.cc1d_floor_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
+        lib.cc1d_floor_chunks.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, vp]
+        for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks):
+            f.restype = i32
+        self.lib = lib
+
+    @staticmethod
+    def _check(rc, name):
+        if rc != 0:
+            raise RuntimeError(f"{name} failed ({rc})")
+
+    def copy(self, torch, src, dst):
+        self._check(self.lib.cc1d_floor_copy(src.data_ptr(), dst.data_ptr(), src.numel() * src.element_size() // 16,
+                                             torch.cuda.current_stream().cuda_stream), "cc1d_floor_copy")
+
+    def rows(self, torch, x, out, pool, idx, ratio):
+        xvec = x.shape[1] * x.element_size() // 16
+        self._check(self.lib.cc1d_floor_rows(x.data_ptr(), out.data_ptr(), pool.data_ptr(), idx.data_ptr(),
+                                             x.shape[0], xvec, pool[0].numel() * pool.element_size() // 16,
+                                             pool.shape[0], ratio, torch.cuda.current_stream().cuda_stream),
+                    "cc1d_floor_rows")
+
+    def chunks(self, torch, x, out, pool, idx, cs, nchunks):
+        line_chunks = pool.shape[2] * pool.element_size() // 16
+        xwords = x.shape[2] * x.element_size() // 4
+        self._check(self.lib.cc1d_floor_chunks(x.data_ptr(), out.data_ptr(), pool.data_ptr(), idx.data_ptr(),
+                                               cs.data_ptr(), x.shape[0], x.shape[1], line_chunks,
+                                               pool[0].numel() * pool.element_size() // 16, pool.shape[0],
+                                               nchunks, xwords, torch.cuda.current_stream().cuda_stream),
+                    "cc1d_floor_chunks")
+
+
+# ------------------------------------------------------------------ C2 step (value)
+
+
+def _c2_sets(torch, n):
+    sets = []
+    for i in range(n):
+        g = torch.Generator(device="cuda").manual_seed(100 + i)
+        x = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
+        dout = torch.randn(B, D, L, generator=g, device="cuda").bfloat16()
+        sets.append((x, dout))
+    g = torch.Generator(device="cuda").manual_seed(0)
+    w = torch.randn(D, W, generator=g, device="cuda").bfloat16()
+    b = torch.randn(D, generator=g, device="cuda").bfloat16()
+    return sets, w, b
 
 
 def bench_step(torch, cc, args, sets, w, b):
@@ -184,106 +279,73 @@ def bench_step(torch, cc, args, sets, w, b):
     return ms
 
 
-def bench_kernels(torch, sets, w, b, launches):
-    """Per-launch duration of the forward and backward kernels (custom ops, no autograd)."""
-    nsets = len(sets)
-    outs = [torch.empty_like(x) for x, _ in sets]
-    dxs = [torch.empty_like(x) for x, _ in sets]
+# ------------------------------------------------------------------ kernel cases
+
+
+def _c2_cases(torch, sets, w, b):
+    """C2 forward, backward (the reference-shaped op: fp32 accumulators) and the autograd
+    backward (typed gradients: backward kernel + fixed-order reduction)."""
+    ops = torch.ops.causal_conv1d_amd
     dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
     db = torch.zeros(D, dtype=torch.float32, device="cuda")
-    xs = [x.detach() for x, _ in sets]
-
-    def fwd_loop():
-        for i in range(launches):
-            torch.ops.causal_conv1d_amd._fwd_inplace(xs[i % nsets], w, b, None, None, outs[i % nsets], True, None)
-
-    def bwd_loop():
-        for i in range(launches):
-            x, dout = xs[i % nsets], sets[i % nsets][1]
-            torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dxs[i % nsets], dw, db, None,
-                                                          True)
-
-    res = {}
-    for name, loop, nbytes in (("fwd", fwd_loop, FWD_BYTES), ("bwd", bwd_loop, BWD_BYTES)):
-        g = _graph(torch, loop)
-        ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
-        res[name] = {"us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
-                     "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                     "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-        log(f"{name}: {res[name]}")
-        del g
-    return res
+    dwt = torch.empty(D, W, dtype=torch.bfloat16, device="cuda")
+    dbt = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    bufs = [(x.detach(), dout, torch.empty_like(x), torch.empty_like(x)) for x, dout in sets]
+    return {
+        "fwd": ([lambda x=x, o=o: ops._fwd_inplace(x, w, b, None, None, o, True, None) for x, _, o, _ in bufs],
+                FWD_BYTES, 1, {}),
+        "bwd": ([lambda x=x, d=d, dx=dx: ops._bwd_full_inplace(x, w, b, d, None, None, dx, dw, db, None, True)
+                 for x, d, _, dx in bufs], BWD_BYTES, 1, {"op": "_bwd_full_inplace (fp32 accumulators)"}),
+        "bwd_typed": ([lambda x=x, d=d, dx=dx: ops._bwd_typed_inplace(x, w, b, d, None, None, None, dx, dwt, dbt,
+                                                                       None, True)
+                       for x, d, _, dx in bufs], BWD_TYPED_BYTES, 1,
+                      {"op": "_bwd_typed_inplace (the autograd backward: bwd_rows_vec + bwd_reduce)"}),
+    }
 
 
-def _update_sets(torch, n):
+def _update_sets(torch, n, seqlen=1, S=W - 1, seed=7):
     sets = []
-    g = torch.Generator(device="cuda").manual_seed(7)
+    g = torch.Generator(device="cuda").manual_seed(seed)
     w = torch.randn(D, W, generator=g, device="cuda").bfloat16()
     b = torch.randn(D, generator=g, device="cuda").bfloat16()
     for _ in range(n):
-        x = torch.randn(UPD_B, D, generator=g, device="cuda").bfloat16()
-        pool = torch.randn(UPD_POOL, D, W - 1, generator=g, device="cuda").bfloat16()
+        x = torch.randn(UPD_B, D, seqlen, generator=g, device="cuda").bfloat16()
+        pool = torch.randn(UPD_POOL, D, S, generator=g, device="cuda").bfloat16()
         idx = torch.randperm(UPD_POOL, generator=g, device="cuda")[:UPD_B].to(torch.int32)
-        sets.append((x, pool, idx, torch.empty_like(x)))
+        cs = torch.randint(0, C4B_S, (UPD_B,), generator=g, device="cuda", dtype=torch.int32)
+        sets.append((x, pool, idx, cs, torch.empty_like(x)))
     return sets, w, b
 
 
-def bench_update(torch, cc, launches):
-    nsets = -(-MALL_BYTES // (UPD_POOL * D * (W - 1) * 2 + 2 * UPD_B * D * 2)) + 1
+def _c4a_cases(torch, cc, floors):
+    """C4a decode (linear, one token) and its floors, over enough rotating sets that the
+    bytes touched between two reuses of a set exceed twice the Infinity Cache."""
+    nsets = -(-2 * MALL_BYTES // UPD_TOUCHED) + 1  # 42
     sets, w, b = _update_sets(torch, nsets)
-    lib_update = cc._native.native_update
-
-    def loop():
-        for i in range(launches):
-            x, pool, idx, out = sets[i % nsets]
-            lib_update(x.unsqueeze(-1), w, b, pool, idx, None, out.unsqueeze(-1), True)
-
-    g = _graph(torch, loop)
-    ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
-    us = ms * 1e3
-    del g
-
-    # A decode loop reuses one state pool every step: with one buffer set the 21 MB of
-    # a call stay in the 256 MB Infinity Cache between calls. Reported beside the
-    # HBM-streaming figure above, never as it.
-    def warm_loop():
-        x, pool, idx, out = sets[0]
-        for _ in range(launches):
-            lib_update(x.unsqueeze(-1), w, b, pool, idx, None, out.unsqueeze(-1), True)
-
-    g = _graph(torch, warm_loop)
-    us_warm = min(_time_graph(torch, g, 3) for _ in range(3)) / launches * 1e3
-    del g
-    res = {"workload": "C4a: x (256,5120,1) bf16, pool (512,5120,3), 256 random rows, W4, bias, SiLU",
-           "us_per_call": round(us, 2), "algorithmic_bytes": UPD_BYTES,
-           "gbps": round(UPD_BYTES / (us * 1e-6) / 1e9, 1),
-           "frac_of_peak": round(UPD_BYTES / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "buffer_sets": nsets,
-           "us_per_call_cache_resident": round(us_warm, 2)}
-    log(f"update: {res}")
-    return res
+    upd = cc._native.native_update
+    cases = {
+        "update_c4a": ([lambda u=u: upd(u[0], w, b, u[1], u[2], None, u[4], True) for u in sets], UPD_BYTES, 1,
+                       {"workload": "C4a: x (256,5120,1) bf16, pool (512,5120,3), 256 random rows, W4, bias, SiLU",
+                        "buffer_sets": nsets,
+                        "bytes_between_reuses": (nsets - 1) * UPD_TOUCHED}),
+        "update_c4a_cache_resident": ([lambda u=sets[0]: upd(u[0], w, b, u[1], u[2], None, u[4], True)], UPD_BYTES,
+                                      1, {"note": "one buffer set reused every call (a decode loop over one layer)"}),
+    }
+    if floors is not None:
+        # a plain copy of the same bytes (10.5 MB read, 10.5 MB written), rotating as the update does
+        half = UPD_BYTES // 2 // 16 * 16
+        cp = [(torch.empty(half, dtype=torch.uint8, device="cuda").fill_(1),
+               torch.empty(half, dtype=torch.uint8, device="cuda")) for _ in range(nsets)]
+        cases["floor_copy_c4a"] = ([lambda a=a, c=c: floors.copy(torch, a, c) for a, c in cp], 2 * half, 1,
+                                   {"note": "plain copy of the update's bytes, one 16-byte vector per lane"})
+        cases["floor_rows_c4a"] = ([lambda u=u: floors.rows(torch, u[0][..., 0], u[4][..., 0], u[1], u[2], W - 1)
+                                    for u in sets], UPD_BYTES, 1,
+                                   {"note": "the update's scattered rows without arithmetic: x row and pool row "
+                                            "idx[b] read, out row and pool row written, all coalesced"})
+    return cases
 
 
-def _time_launch_set(torch, fns, launches):
-    """Average ms per launch of a graph that cycles through the closures `fns`."""
-    def loop():
-        for i in range(launches):
-            fns[i % len(fns)]()
-    g = _graph(torch, loop)
-    ms = min(_time_graph(torch, g, 3) for _ in range(3)) / launches
-    del g
-    return ms
-
-
-def _entry(ms, nbytes, **extra):
-    gbps = nbytes / (ms * 1e-3) / 1e9
-    return {"us_per_launch": round(ms * 1e3, 2), "algorithmic_bytes": int(nbytes), "gbps": round(gbps, 1),
-            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), **extra}
-
-
-def _config_cases(torch, cc):
-    """Launch closures of the other benchmark configurations: name -> (closures cycling
-    over rotating buffer sets, algorithmic bytes per launch, launches per timing graph
-    divisor, extra report fields)."""
+def _c3_cases(torch):
     ops = torch.ops.causal_conv1d_amd
     cases = {}
     # C3: stored (1, 8192, 4096) bf16 channel-last, viewed (1, 4096, 8192); W4, SiLU, no bias
@@ -297,141 +359,227 @@ def _config_cases(torch, cc):
         seq[:, c:] = i + 1
     seq = seq.cuda()
     init = torch.randn(1, D3, W - 1, generator=g, device="cuda").bfloat16()
-    for _ in range(3):
+    for _ in range(4):
         x = torch.randn(1, L3, D3, generator=g, device="cuda").bfloat16().transpose(1, 2)
         dout = torch.randn(1, L3, D3, generator=g, device="cuda").bfloat16().transpose(1, 2)
         sets.append((x, dout, torch.empty_like(x), torch.empty_like(x)))
     dw3 = torch.zeros(D3, W, dtype=torch.float32, device="cuda")
+    dw3t = torch.empty(D3, W, dtype=torch.bfloat16, device="cuda")
     fs = torch.empty(1, D3, W - 1, dtype=torch.bfloat16, device="cuda")
     di = torch.empty_like(init)
     n3 = L3 * D3 * 2
-    for name, kw_f, kw_b, extra_f, extra_b in (
-            ("c3a", (seq, None, None), (seq, None), 32768 + D3 * W * 2, 2 * 32768 + D3 * W * 2 + D3 * W * 4),
-            ("c3b", (None, init, fs), (None, init), D3 * W * 2 + 2 * 24576, D3 * W * 2 + D3 * W * 4 + 2 * 24576)):
+    for name, kw_f, kw_b, extra_f, extra_b, extra_t in (
+            ("c3a", (seq, None, None), (seq, None), 32768 + D3 * W * 2, 2 * 32768 + D3 * W * 2 + D3 * W * 4,
+             2 * 32768 + 2 * D3 * W * 2),
+            ("c3b", (None, init, fs), (None, init), D3 * W * 2 + 2 * 24576, D3 * W * 2 + D3 * W * 4 + 2 * 24576,
+             2 * D3 * W * 2 + 2 * 24576)):
         s_, i_, f_ = kw_f
         fns = [lambda x=x, o=o, s_=s_, i_=i_, f_=f_: ops._fwd_inplace(x, w3, None, s_, i_, o, True, f_)
                for x, _, o, _ in sets]
         cases[f"{name}_fwd"] = (fns, 2 * n3 + extra_f, 1, {})
         sb, ib = kw_b
-        fns = [lambda x=x, d=d, dx=dx, sb=sb, ib=ib: ops._bwd_full_inplace(x, w3, None, d, sb, ib, dx, dw3, None,
-                                                                           di if ib is not None else None, True)
-               for x, d, _, dx in sets]
-        cases[f"{name}_bwd"] = (fns, 3 * n3 + extra_b, 1, {})
-    # C5: (8, 2048, 16384), no bias, no activation, bf16 and fp32 at W4 (W2/W3 in the tests)
+        dib = di if ib is not None else None
+        fns = [lambda x=x, d=d, dx=dx, sb=sb, ib=ib, dib=dib: ops._bwd_full_inplace(
+            x, w3, None, d, sb, ib, dx, dw3, None, dib, True) for x, d, _, dx in sets]
+        cases[f"{name}_bwd"] = (fns, 3 * n3 + extra_b, 1, {"op": "_bwd_full_inplace (fp32 accumulators)"})
+        fns = [lambda x=x, d=d, dx=dx, sb=sb, ib=ib, dib=dib: ops._bwd_typed_inplace(
+            x, w3, None, d, sb, ib, None, dx, dw3t, None, dib, True) for x, d, _, dx in sets]
+        cases[f"{name}_bwd_typed"] = (fns, 3 * n3 + extra_t, 1,
+                                      {"op": "_bwd_typed_inplace (the autograd backward: bwd_cl + bwd_reduce)"})
+    return cases, (cuts, L3, D3)
+
+
+def _c5_cases(torch):
+    """C5: (8, 2048, 16384), no bias, no activation, forward and backward for every dtype and
+    width of the configuration."""
+    ops = torch.ops.causal_conv1d_amd
     B5, D5, L5 = 8, 2048, 16384
-    for dt, tag in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
-        es = 2 if dt == torch.bfloat16 else 4
+    cases = {}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for dt, tag in ((torch.float32, "fp32"), (torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        es = torch.finfo(dt).bits // 8
         x = torch.randn(B5, D5, L5, generator=g, device="cuda").to(dt)
         dout = torch.randn(B5, D5, L5, generator=g, device="cuda").to(dt)
         out, dx = torch.empty_like(x), torch.empty_like(x)
-        w5 = torch.randn(D5, W, generator=g, device="cuda").to(dt)
-        dw5 = torch.zeros(D5, W, dtype=torch.float32, device="cuda")
         n5 = B5 * D5 * L5 * es
-        cases[f"c5_{tag}_fwd"] = ([lambda x=x, w5=w5, out=out: ops._fwd_inplace(x, w5, None, None, None, out, False,
-                                                                                 None)], 2 * n5 + D5 * W * es, 8, {})
-        cases[f"c5_{tag}_bwd"] = ([lambda x=x, w5=w5, dout=dout, dx=dx, dw5=dw5: ops._bwd_full_inplace(
-            x, w5, None, dout, None, None, dx, dw5, None, None, False)], 3 * n5 + D5 * W * (es + 4), 8, {})
-    # C4b: x (256, 5120, 4), circular state_len 64 in a pool of 512, cache_seqlens in [0, 64)
-    usets = []
-    w4 = torch.randn(D, W, generator=g, device="cuda").bfloat16()
-    b4 = torch.randn(D, generator=g, device="cuda").bfloat16()
-    for _ in range(4):
-        x = torch.randn(UPD_B, D, 4, generator=g, device="cuda").bfloat16()
-        pool = torch.randn(UPD_POOL, D, 64, generator=g, device="cuda").bfloat16()
-        idx = torch.randperm(UPD_POOL, generator=g, device="cuda")[:UPD_B].to(torch.int32)
-        cs = torch.randint(0, 64, (UPD_B,), generator=g, device="cuda", dtype=torch.int32)
-        usets.append((x, pool, idx, cs, torch.empty_like(x)))
-    fns = [lambda u=u: cc._native.native_update(u[0], w4, b4, u[1], u[2], u[3], u[4], True) for u in usets]
-    nb = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4
-    cases["update_c4b"] = (fns, nb, 1, {"note": "14 of 128 bytes of each state row are touched; DRAM bursts "
-                                                "bound this"})
-    # varlen states: x (8192, 4096) bf16 packing the 8 C3 sequences, state_len W-1
+        for w_ in (2, 3, 4):
+            w5 = torch.randn(D5, w_, generator=g, device="cuda").to(dt)
+            dw5 = torch.zeros(D5, w_, dtype=torch.float32, device="cuda")
+            cases[f"c5_{tag}_w{w_}_fwd"] = ([lambda x=x, w5=w5, out=out: ops._fwd_inplace(
+                x, w5, None, None, None, out, False, None)], 2 * n5 + D5 * w_ * es, 8, {})
+            cases[f"c5_{tag}_w{w_}_bwd"] = ([lambda x=x, w5=w5, dout=dout, dx=dx, dw5=dw5: ops._bwd_full_inplace(
+                x, w5, None, dout, None, None, dx, dw5, None, None, False)], 3 * n5 + D5 * w_ * (es + 4), 8, {})
+    return cases
+
+
+def _c4b_cases(torch, cc, floors):
+    """C4b: x (256, 5120, 4), circular state_len 64 in a pool of 512, cache_seqlens in [0, 64)."""
+    nsets = -(-2 * MALL_BYTES // C4B_LINE_BYTES) + 1  # 5: whole lines touched between reuses > 2x MALL
+    sets, w, b = _update_sets(torch, nsets, seqlen=4, S=C4B_S, seed=11)
+    fns = [lambda u=u: cc._native.native_update(u[0], w, b, u[1], u[2], u[3], u[4], True) for u in sets]
+    hbm = _pmc("update_c4b")
+    extra = {"buffer_sets": nsets, "note": "14 of 128 bytes of each state line are touched; DRAM bursts bound this"}
+    cases = {"update_c4b": (fns, C4B_BYTES, 1, extra)}
+    if floors is not None:
+        for nch in (1, 2):
+            cases[f"floor_chunks{nch}_c4b"] = (
+                [lambda u=u, nch=nch: floors.chunks(torch, u[0], u[4], u[1], u[2], u[3], nch) for u in sets],
+                C4B_BYTES, 1, {"note": f"{nch} 16-byte chunk(s) of each state line read and written back, x / out "
+                                       "moved, no arithmetic"})
+    return cases, hbm
+
+
+def _varlen_case(torch, cc, c3info):
+    cuts, L3, D3 = c3info
+    g = torch.Generator(device="cuda").manual_seed(9)
     xv = torch.randn(L3, D3, generator=g, device="cuda").bfloat16()
     cu = torch.tensor([0] + cuts.tolist() + [L3], dtype=torch.int32, device="cuda")
     nseq = cu.numel() - 1
     st = torch.empty(nseq, W - 1, D3, dtype=torch.bfloat16, device="cuda").transpose(1, 2)
-    cases["varlen_states"] = ([lambda: cc._native.native_varlen_states(xv, cu, st)],
+    return {"varlen_states": ([lambda: cc._native.native_varlen_states(xv, cu, st)],
                               2 * nseq * (W - 1) * D3 * 2 + cu.numel() * 4, 1,
-                              {"note": "gathers 8 x 3 rows of 4096 channels (197 KB each way): launch-bound"})
-    return cases
+                              {"note": "gathers 8 x 3 rows of 4096 channels (197 KB each way): launch-bound"})}
 
 
-def bench_configs(torch, cc, launches):
-    """Kernel throughput at the other benchmark configurations (reported, not the headline)."""
+def _run_cases(torch, cases, launches, runs, res):
+    for name, (fns, nbytes, div, extra) in cases.items():
+        us = _time_launch_set(torch, fns, max(4, launches // div), runs)
+        res[name] = _entry(us, nbytes, **extra)
+        log(f"{name}: {res[name]['us_per_launch']} us/launch (min {res[name]['us_min']}, max {res[name]['us_max']}; "
+            f"{res[name]['frac_of_peak']:.3f} of peak)")
+
+
+def bench_configs(torch, cc, floors, args):
+    """Every kernel at the other benchmark configurations (reported, not the headline)."""
     res = {}
-    for name, (fns, nbytes, div, extra) in _config_cases(torch, cc).items():
-        ms = _time_launch_set(torch, fns, max(4, launches // div))
-        res[name] = _entry(ms, nbytes, **extra)
-        if name == "update_c4b":
-            res[name]["us_per_call"] = res[name]["us_per_launch"]
-        log(f"{name}: {res[name]['us_per_launch']} us/launch ({res[name]['frac_of_peak']:.3f} of peak)")
+    c3, c3info = _c3_cases(torch)
+    _run_cases(torch, c3, args.launches, args.runs, res)
+    del c3
+    torch.cuda.empty_cache()
+    c5 = _c5_cases(torch)
+    _run_cases(torch, c5, args.launches, args.runs, res)
+    del c5
+    torch.cuda.empty_cache()
+    c4b, hbm = _c4b_cases(torch, cc, floors)
+    _run_cases(torch, c4b, args.launches, args.runs, res)
+    e = res["update_c4b"]
+    e["us_per_call"] = e["us_per_launch"]
+    if hbm:
+        # HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated)
+        e["hbm_bytes_per_launch"] = int(hbm)
+        e["hbm_gbps"] = round(hbm / (e["us_per_launch"] * 1e-6) / 1e9, 1)
+        e["hbm_frac_of_peak"] = round(e["hbm_gbps"] / HBM_PEAK_GBPS, 4)
+    if "floor_chunks2_c4b" in res:
+        e["floor_chunks1_us"] = res["floor_chunks1_c4b"]["us_per_launch"]
+        e["floor_chunks2_us"] = res["floor_chunks2_c4b"]["us_per_launch"]
+    del c4b
+    torch.cuda.empty_cache()
+    _run_cases(torch, _varlen_case(torch, cc, c3info), args.launches, args.runs, res)
     return res
 
 
-def cpu_baseline(torch, seconds):
-    """The CPU oracle on a bounded sample of C2 (512 of the 5120 channels, all 4
-    batches, full length), fwd + bwd repeated for about `seconds`."""
-    from oracle import oracle as O
+# ------------------------------------------------------------------ CPU baseline
 
-    d = 512
+
+def _cpu_model():
+    model, fam, mod, step = "unknown", None, None, None
+    try:
+        for ln in open("/proc/cpuinfo"):
+            k, _, v = ln.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            elif k == "cpu family" and fam is None:
+                fam = v
+            elif k == "model" and mod is None:
+                mod = v
+            elif k == "stepping" and step is None:
+                step = v
+    except OSError:
+        pass
+    return f"{model} (family {fam}, model {mod}, stepping {step})"
+
+
+def _cpu_sample(torch, d):
     g = torch.Generator().manual_seed(0)
     x = torch.randn(B, d, L, generator=g).bfloat16()
     w = torch.randn(d, W, generator=g).bfloat16()
     b = torch.randn(d, generator=g).bfloat16()
-    dout = torch.randn(B, d, L, generator=g).bfloat16()
-    out = torch.empty_like(x)
-    dx = torch.empty_like(x)
-    nbytes = (FWD_BYTES + BWD_BYTES) * d / D
+    dout = torch.randn(B, d, L, generator=torch.Generator().manual_seed(1)).bfloat16()
+    return x, w, b, dout
+
+
+def _repeat(fn, seconds, max_reps=10000):
     reps, t0 = 0, time.perf_counter()
     while True:
-        O.fwd(x, w, b, None, None, out, True)
-        dw = torch.zeros(d, W)
-        db = torch.zeros(d)
-        O.bwd(x, w, b, dout, None, None, dx, dw, db, None, True)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and reps >= 3) or reps >= 10000:
-            break
+        if (el >= seconds and reps >= 3) or reps >= max_reps:
+            return reps, el
+
+
+def cpu_baseline(torch, seconds):
+    """Two legs on the same bounded sample of C2 (512 of the 5120 channels, all 4 batches,
+    full length), fwd + bwd repeated for about `seconds` each:
+      * the C oracle, which restates the reference's Mojo CPU kernels (OpenMP over rows);
+      * the reference's pure-PyTorch baseline, F.conv1d(groups=D) + F.silu with autograd
+        (scripts/plot_bench.py:165-169), on torch's CPU threads."""
+    import torch.nn.functional as F
+
+    from oracle import oracle as O
+
+    d = 512
+    x, w, b, dout = _cpu_sample(torch, d)
+    nbytes = (FWD_BYTES + BWD_BYTES) * d / D
+    out, dx = torch.empty_like(x), torch.empty_like(x)
+
+    def port():
+        O.fwd(x, w, b, None, None, out, True)
+        O.bwd(x, w, b, dout, None, None, dx, torch.zeros(d, W), torch.zeros(d), None, True)
+
+    reps, el = _repeat(port, seconds)
     per = el / reps
     res = {"value": round(nbytes / per / 1e9, 2), "unit": "GB/s", "cores": O.num_threads(), "kind": "port",
            "sample": f"C2 fwd+bwd restricted to 512 of 5120 channels (x (4,512,2048) bf16), {reps} reps "
                      f"in {el:.1f} s, {per * 1e3:.1f} ms per fwd+bwd; C oracle restating the reference's "
                      f"Mojo CPU kernels (the Mojo path itself cannot be built here)",
            "cpu_model": _cpu_model()}
+
+    xg, wg, bg = (t.clone().requires_grad_() for t in (x, w, b))
+
+    def torch_ref():
+        o = F.silu(F.conv1d(xg, wg.unsqueeze(1), bg, padding=W - 1, groups=d)[..., :L])
+        torch.autograd.grad(o, (xg, wg, bg), dout)
+
+    reps, el = _repeat(torch_ref, seconds)
+    per = el / reps
+    res["torch_cpu"] = {"value": round(nbytes / per / 1e9, 2), "unit": "GB/s", "threads": torch.get_num_threads(),
+                        "sample": f"same sample, bf16 F.conv1d + F.silu forward and autograd backward, {reps} reps "
+                                  f"in {el:.1f} s, {per * 1e3:.1f} ms per fwd+bwd"}
     log(f"cpu baseline: {res}")
     return res
 
 
-def _cpu_model():
-    try:
-        for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                return ln.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+# ------------------------------------------------------------------ modes
 
 
-def mode_kernels(torch, cc, args):
+def mode_kernels(torch, cc, floors, args):
     """Eager launch loop (for rocprofv3 kernel traces / counters)."""
-    sets, w, b = _c2_sets(torch, 3)
-    outs = [torch.empty_like(x) for x, _ in sets]
-    dxs = [torch.empty_like(x) for x, _ in sets]
-    dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
-    db = torch.zeros(D, dtype=torch.float32, device="cuda")
-    usets, uw, ub = _update_sets(torch, 13)
-    cases = {} if args.no_configs else _config_cases(torch, cc)
+    sets, w, b = _c2_sets(torch, 4)
+    cases = dict(_c2_cases(torch, sets, w, b))
+    cases.update(_c4a_cases(torch, cc, floors))
+    if not args.no_configs:
+        c3, c3info = _c3_cases(torch)
+        cases.update(c3)
+        cases.update(_c5_cases(torch))
+        cases.update(_c4b_cases(torch, cc, floors)[0])
+        cases.update(_varlen_case(torch, cc, c3info))
     for i in range(args.steps):
-        x, dout = sets[i % 3]
-        torch.ops.causal_conv1d_amd._fwd_inplace(x, w, b, None, None, outs[i % 3], True, None)
-        torch.ops.causal_conv1d_amd._bwd_full_inplace(x, w, b, dout, None, None, dxs[i % 3], dw, db, None, True)
-        ux, pool, idx, uo = usets[i % 13]
-        cc._native.native_update(ux.unsqueeze(-1), uw, ub, pool, idx, None, uo.unsqueeze(-1), True)
         for fns, _, _, _ in cases.values():
             fns[i % len(fns)]()
     torch.cuda.synchronize()
-    log(f"kernels mode: {args.steps} iterations of fwd + bwd + update" + ("" if args.no_configs else
-        " + the C3 / C5 / C4b launches") + " done")
+    log(f"kernels mode: {args.steps} iterations of {len(cases)} cases done: {', '.join(cases)}")
 
 
 def mode_copy(torch, args):
@@ -459,20 +607,30 @@ def main():
     from causal_conv1d_amd import _lib
 
     _lib.load()  # fail loudly if the HIP library is missing
+    floors = Floors()
     if args.mode == "kernels":
-        return mode_kernels(torch, cc, args)
+        return mode_kernels(torch, cc, floors, args)
     if args.mode == "copy":
         return mode_copy(torch, args)
 
-    nsets = max(2, -(-MALL_BYTES // (4 * B * D * L * 2)) + 1)
+    nsets = 4  # 3 other sets between reuses: 504 MB for the forward, 755 MB for the backward
     sets, w, b = _c2_sets(torch, nsets)
     ms = bench_step(torch, cc, args, sets, w, b)
-    kern = bench_kernels(torch, sets, w, b, args.launches)
+    kern = {}
+    _run_cases(torch, _c2_cases(torch, sets, w, b), args.launches, args.runs, kern)
+    for k in ("fwd", "bwd", "bwd_typed"):
+        kern[k]["buffer_sets"] = nsets
     del sets
     torch.cuda.empty_cache()
-    upd = bench_update(torch, cc, args.launches)
+    _run_cases(torch, _c4a_cases(torch, cc, floors), args.launches, args.runs, kern)
+    u = kern["update_c4a"]
+    u["us_per_call"] = u["us_per_launch"]
+    u["us_per_call_cache_resident"] = kern.pop("update_c4a_cache_resident")["us_per_launch"]
+    u["floor_copy_us"] = kern["floor_copy_c4a"]["us_per_launch"]
+    u["floor_rows_us"] = kern["floor_rows_c4a"]["us_per_launch"]
     torch.cuda.empty_cache()
-    cfgs = {} if args.no_configs else bench_configs(torch, cc, args.launches)
+    if not args.no_configs:
+        kern.update(bench_configs(torch, cc, floors, args))
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else cpu_baseline(torch, args.cpu_seconds)
 
@@ -496,7 +654,7 @@ def main():
             "workload": "C2: causal_conv1d_fn fwd + autograd bwd, x (4,5120,2048) bf16 channel-first, "
                         "weight (5120,4), bias, SiLU; a HIP graph of one step per rotating buffer set",
             "batch": B, "dim": D, "seqlen": L, "width": W, "accumulate": "fp32",
-            "step_algorithmic_bytes": step_bytes,
+            "step_algorithmic_bytes": step_bytes, "buffer_sets": nsets,
         },
         "roofline": {
             "bound": "hbm",
@@ -505,11 +663,13 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(bwd["gbps"] / HBM_PEAK_GBPS, 4),
-            "traffic": _pmc_traffic("bwd"),
+            "traffic": _pmc("bwd"),
             "algorithmic_bytes_per_launch": BWD_BYTES,
             "us_per_launch": bwd["us_per_launch"],
+            "us_min": bwd["us_min"],
+            "us_max": bwd["us_max"],
         },
-        "kernels": {"fwd": kern["fwd"], "bwd": kern["bwd"], "update_c4a": upd, **cfgs},
+        "kernels": kern,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,0 +1,149 @@
+// cc1d_floor.hip -- bandwidth floors for bench.py (measurement only; the
+// product library does not contain or call these kernels).
+//
+// Each kernel moves the bytes of one decode-update configuration with no
+// arithmetic, so its time is what HBM and the launch cost for that access
+// pattern on this GPU. Every store writes a value that differs from what was
+// loaded (bits flipped), so no store can be dropped as a no-op.
+//
+//   cc1d_floor_copy   -- a plain streaming copy of n 16-byte vectors: one
+//                        vector per lane, 64-thread blocks (the fastest shape
+//                        measured for ~10 MB copies).
+//   cc1d_floor_rows   -- the scattered-row pattern of the linear decode
+//                        update: for each batch entry b, read x row b and
+//                        pool row idx[b], write out row b and pool row idx[b]
+//                        back in place; one wavefront per 64 x vectors and
+//                        the 64 * R state vectors of the same channels, all
+//                        accesses coalesced.
+//   cc1d_floor_chunks -- the circular decode update's pattern: per (b, c),
+//                        read and write back `chunks` consecutive 16-byte
+//                        chunks of state line (idx[b], c) starting at chunk
+//                        cs[b] mod line_chunks (wrapping), and read x / write
+//                        out `xwords` dwords.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+namespace {
+
+__device__ __forceinline__ u32x4 flip(u32x4 v) {
+    const u32x4 one = {1u, 1u, 1u, 1u};
+    return v ^ one;
+}
+
+__global__ void __launch_bounds__(64) floor_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (i < n) dst[i] = flip(src[i]);
+}
+
+// one wavefront per (entry, group of 64 x vectors): lane l moves x vector l
+// and state vectors l, l+64, ..., l+64(R-1) of the group's state span
+// (grid: groups x batch entries, so no division). Every access is
+// unconditional, at a clamped in-bounds address (a lane past the end reads
+// and writes the last vector again, with the same value as its owner), so the
+// compiler can neither sink a load into a branch nor serialise the loads:
+// x first, then the index as a scalar load behind a scheduling fence, then
+// the state loads, and the stores behind a second fence. An index outside
+// [0, pool_rows) is clamped to row 0 (bench.py passes permutations only).
+template <int R>
+__global__ void __launch_bounds__(64) floor_rows(const u32x4* __restrict__ x, u32x4* __restrict__ out,
+                                                 u32x4* __restrict__ pool, const int32_t* __restrict__ idx,
+                                                 uint32_t xvec, uint32_t pool_row_vec, int32_t pool_rows) {
+    const int lane = threadIdx.x;
+    const uint32_t b = blockIdx.y;
+    const uint32_t g = blockIdx.x;
+    const uint32_t xi = min(g * 64 + lane, xvec - 1);
+    const u32x4 xv = x[(size_t)b * xvec + xi];
+    __builtin_amdgcn_sched_barrier(0);
+    const int32_t r = *(const __attribute__((address_space(4))) int32_t*)(idx + b);
+    u32x4* sr = pool + (size_t)(r >= 0 && r < pool_rows ? r : 0) * pool_row_vec + g * 64 * R;
+    const uint32_t nsv = (xvec - g * 64) * R;  // state vectors left in this row from the group's start
+    u32x4 sv[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) sv[j] = sr[min((uint32_t)(j * 64 + lane), nsv - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    out[(size_t)b * xvec + xi] = flip(xv);
+#pragma unroll
+    for (int j = 0; j < R; ++j) sr[min((uint32_t)(j * 64 + lane), nsv - 1)] = flip(sv[j]);
+}
+
+__global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__ x, uint32_t* __restrict__ out,
+                                                    u32x4* __restrict__ pool, const int32_t* __restrict__ idx,
+                                                    const int32_t* __restrict__ cs, int64_t batch, int64_t dim,
+                                                    int64_t line_chunks, int64_t pool_row_chunks, int64_t pool_rows,
+                                                    int chunks, int xwords) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= batch * dim) return;
+    const int64_t b = t / dim;
+    const int64_t c = t - b * dim;
+    uint32_t xv[4];
+    for (int i = 0; i < xwords; ++i) xv[i] = x[t * xwords + i];
+    const int32_t row = idx[b];
+    if (row < 0 || row >= pool_rows) return;
+    int64_t k = cs[b] % line_chunks;
+    if (k < 0) k += line_chunks;
+    u32x4* line = pool + (int64_t)row * pool_row_chunks + c * line_chunks;
+    u32x4 v[2];
+    for (int j = 0; j < chunks; ++j) v[j] = line[(k + j) % line_chunks];
+    for (int i = 0; i < xwords; ++i) out[t * xwords + i] = xv[i] ^ 1u;
+    for (int j = 0; j < chunks; ++j) line[(k + j) % line_chunks] = flip(v[j]);
+}
+
+bool launched() { return hipGetLastError() == hipSuccess; }
+
+}  // namespace
+
+extern "C" {
+
+// 0 on success, -1 on a bad argument, -2 if the launch failed
+int cc1d_floor_copy(const void* src, void* dst, int64_t n16, void* stream) {
+    if (n16 < 0 || (n16 > 0 && (src == nullptr || dst == nullptr))) return -1;
+    if (n16 == 0) return 0;
+    floor_copy<<<dim3((unsigned)((n16 + 63) / 64)), 64, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), n16);
+    return launched() ? 0 : -2;
+}
+
+// x, out: (batch, xvec) 16-byte vectors; pool: pool_rows rows of pool_row_vec
+// vectors, of which the first xvec * ratio are the state span; idx: (batch,)
+// rows in [0, pool_rows) (others are clamped to row 0)
+int cc1d_floor_rows(const void* x, void* out, void* pool, const int32_t* idx, int64_t batch, int64_t xvec,
+                    int64_t pool_row_vec, int64_t pool_rows, int ratio, void* stream) {
+    if (batch < 0 || batch > 65535 || xvec < 0 || ratio < 1 || ratio > 4 || pool_row_vec < xvec * ratio ||
+        pool_row_vec >= ((int64_t)1 << 32) || pool_rows >= ((int64_t)1 << 31))
+        return -1;
+    if (batch == 0 || xvec == 0) return 0;
+    if (x == nullptr || out == nullptr || pool == nullptr || idx == nullptr) return -1;
+    const dim3 grid((unsigned)((xvec + 63) / 64), (unsigned)batch);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const u32x4* xv = static_cast<const u32x4*>(x);
+    u32x4* ov = static_cast<u32x4*>(out);
+    u32x4* pv = static_cast<u32x4*>(pool);
+    switch (ratio) {
+    case 1: floor_rows<1><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
+    case 2: floor_rows<2><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
+    case 3: floor_rows<3><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
+    default: floor_rows<4><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
+    }
+    return launched() ? 0 : -2;
+}
+
+// pool: pool_rows rows of pool_row_chunks 16-byte chunks, dim lines of
+// line_chunks chunks each; x, out: (batch, dim) items of xwords dwords; chunks
+// in {1, 2}; xwords in 1..4; idx entries outside [0, pool_rows) are skipped
+int cc1d_floor_chunks(const void* x, void* out, void* pool, const int32_t* idx, const int32_t* cs, int64_t batch,
+                      int64_t dim, int64_t line_chunks, int64_t pool_row_chunks, int64_t pool_rows, int chunks,
+                      int xwords, void* stream) {
+    if (batch < 0 || dim < 0 || line_chunks < 2 || chunks < 1 || chunks > 2 || xwords < 1 || xwords > 4 ||
+        pool_row_chunks < dim * line_chunks)
+        return -1;
+    if (batch == 0 || dim == 0) return 0;
+    if (x == nullptr || out == nullptr || pool == nullptr || idx == nullptr || cs == nullptr) return -1;
+    floor_chunks<<<dim3((unsigned)((batch * dim + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint32_t*>(x), static_cast<uint32_t*>(out), static_cast<u32x4*>(pool), idx, cs, batch, dim,
+        line_chunks, pool_row_chunks, pool_rows, chunks, xwords);
+    return launched() ? 0 : -2;
+}
+
+}  // extern "C"

@@ -3,7 +3,9 @@
 Each ``*.hip`` translation unit in this directory is compiled to an object
 with hipcc (in parallel), then linked into
 ``causal_conv1d_amd/_lib/libcc1d_amd.so``. The library exposes only the
-``extern "C"`` entry points of ``include/cc1d.h``.
+``extern "C"`` entry points of ``include/cc1d.h``. ``bench/cc1d_floor.hip``
+(bandwidth floors that ``bench.py`` times beside the kernels) is linked on
+its own into ``causal_conv1d_amd/_lib/libcc1d_floor.so``.
 
 Usage: ``python causal-conv1d-mojo_amd/csrc/build.py [--jobs N] [--verbose]``.
 """
@@ -25,6 +27,9 @@ INCLUDE = REPO / "include"
 OBJ_DIR = CSRC / "_build"
 LIB_DIR = PKG_ROOT / "causal_conv1d_amd" / "_lib"
 LIB_PATH = LIB_DIR / "libcc1d_amd.so"
+# bandwidth floors for bench.py (measurement only; not part of the product library)
+FLOOR_SRC = CSRC / "bench" / "cc1d_floor.hip"
+FLOOR_PATH = LIB_DIR / "libcc1d_floor.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -68,24 +73,30 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library. Returns its path."""
-    if HIPCC is None or not Path(HIPCC).exists():
-        raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
-    OBJ_DIR.mkdir(parents=True, exist_ok=True)
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    srcs = _sources()
-    jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 1))
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _link(objs: list[Path], out: Path, verbose: bool) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every HIP source and link the shared library (and the bench's
+    floor library). Returns the product library's path."""
+    if HIPCC is None or not Path(HIPCC).exists():
+        raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = _sources() + [FLOOR_SRC]
+    jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+    _link(objs[:-1], LIB_PATH, verbose)
+    _link(objs[-1:], FLOOR_PATH, verbose)
     return LIB_PATH
 
 

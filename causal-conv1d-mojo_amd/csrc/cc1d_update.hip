@@ -11,10 +11,11 @@
 //   out-of-pool index zeroes out[b] and leaves the pool untouched.
 //
 // Kernels
-//   update_vec1    -- linear mode, one token, S == W-1, channel-contiguous x /
-//                     out and contiguous state rows: a lane owns EPV adjacent
-//                     channels of 2 batch entries, so x, out, weight and the
-//                     (EPV x S) state blocks move as 16-byte vectors.
+//   update_lin     -- linear mode, one token, S == W-1, channel-contiguous x /
+//                     out and contiguous state rows: one wavefront per (batch
+//                     entry, 16 * EPV channels) moves the group's state and x
+//                     spans as consecutive 16-byte vectors, one per lane at
+//                     W = 4, and exchanges them through LDS.
 //   update_circ_vec -- circular mode on contiguous state lines of whole
 //                     16-byte chunks: two adjacent lanes per (b, c) read the
 //                     two chunks that hold its window (one 32-byte access),
@@ -31,7 +32,6 @@ namespace cc1d {
 struct UpdArgs {
     cc1d_update_params p;
     int64_t n_items;
-    int64_t ngroups;  // channel groups per batch row (vec1)
 };
 
 __device__ __forceinline__ int64_t state_row(const cc1d_update_params& p, int64_t b) {
@@ -106,88 +106,168 @@ __global__ void __launch_bounds__(256) update_generic(const UpdArgs a) {
     }
 }
 
-// Linear mode, seqlen 1, state_len == W-1. A lane owns EPV adjacent channels
-// of BPL consecutive batch entries: the weight/bias vectors are loaded once
-// for the BPL entries, and all loads are issued unconditionally (entries
-// past the batch or padding entries read row 0 / entry 0) before the
-// arithmetic; only the stores are predicated. Lanes run along channels, so
-// x, out and the (EPV x S) state blocks of one entry are contiguous spans.
-template <typename T, int W, bool SILU, int BPL, bool UB>
-__global__ void __launch_bounds__(256) update_vec1(const UpdArgs a) {
+// Arguments of update_lin: only what it reads, packed so that one batch of
+// scalar loads fetches all of them (the full params struct took two
+// dependent rounds of kernel-argument loads before the first data load).
+template <typename T> struct LinArgs {
+    const T* x;
+    const T* weight;
+    const T* bias;
+    T* conv_state;
+    const int32_t* idx;
+    T* out;
+    uint32_t x_row, out_row, state_row;  // row strides (elements) of x, out, the state pool
+    uint32_t dim;
+    int32_t state_rows;
+    int32_t unused;
+};
+
+// Linear mode, seqlen 1, state_len == W-1 (H), channel-contiguous x / out and
+// contiguous state rows. One wavefront per (batch entry, group of
+// NCH = 16 * EPV * NV channels): the group's state span (NCH * H elements) and
+// its x span (NCH elements) are 16 * W * NV vectors of 16 bytes, [state | x],
+// and lane l loads vectors l, l + 64, ... of that segment, so every load and store
+// instruction of the wavefront covers consecutive 16-byte vectors (a lane
+// owning whole channels instead reads H vectors at a stride of H vectors:
+// ~1 us slower at C4a). x, the weights and the bias are loaded first, then
+// the pool index (a scalar load) that the state loads wait for. The segment goes
+// through LDS so that each lane takes the H * NV dwords of state and the NV
+// dwords of x of its channels (2 NV for 16-bit types, NV for fp32), computes
+// their outputs and new state, and puts them back; the stores read the segment back
+// in vector order. The state shift moves raw bits, so state values are kept
+// bit for bit. The grid is (channel groups, batch entries).
+template <typename T, int W, int NV, bool SILU, bool HAS_BIAS, bool HAS_IDX>
+__global__ void __launch_bounds__(64) update_lin(const LinArgs<T> a) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
-    constexpr int NV = H;  // 16-byte vectors in an (EPV x H) state block
-    const cc1d_update_params& p = a.p;
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
-    if (idx >= (uint32_t)a.n_items) return;
-    const uint32_t ng = (uint32_t)a.ngroups;
-    // UB: ngroups is a multiple of 64, so a wavefront never straddles two
-    // batch entries; b0 is then wave-uniform and the pool indices are scalar loads
-    const uint32_t b0 = UB ? uniform32((idx / ng) * BPL) : (idx / ng) * BPL;
-    const uint32_t c0 = (idx - (idx / ng) * ng) * EPV;
-    const uint32_t nb = (uint32_t)p.batch;
-
-    const T* wp = static_cast<const T*>(p.weight) + (size_t)c0 * W;
-    u32x4 wv[W];
+    constexpr int NCH = 16 * EPV * NV;       // channels per wavefront
+    constexpr int NSV = 16 * H * NV;         // state vectors in the segment
+    constexpr int NTV = 16 * W * NV;         // all vectors (state, then x)
+    constexpr int NSLOT = (NTV + 63) / 64;   // vectors per lane
+    constexpr int CPL = EPV / 4 * NV;        // channels per lane
+    constexpr int XD = NV;                   // dwords of x (and of out) per lane
+    constexpr int SD = H * NV;               // dwords of state per lane
+    __shared__ u32x4 seg[64 * NSLOT];
+    const int lane = threadIdx.x;
+    const uint32_t b = blockIdx.y;            // batch entry
+    const uint32_t c0 = blockIdx.x * NCH;     // first channel of the group
+    const uint32_t nch = min(a.dim - c0, (uint32_t)NCH);  // channels of this group
+    const int32_t nxv = (int32_t)(nch / EPV), nsv = (int32_t)(nch * H / EPV);  // valid x / state vectors
+    const T* xr = a.x + (size_t)b * a.x_row + c0;
+    // Every lane of a slot that holds x vectors loads one, unconditionally: a
+    // lane of the state part (or past the group's end) reads an in-bounds x
+    // vector of the group and drops it. With no branch around them, the
+    // loads are issued before the pool index arrives.
+    u32x4 xv[NSLOT];
 #pragma unroll
-    for (int n = 0; n < W; ++n) wv[n] = vload(wp + n * EPV);
-    const u32x4 bv = p.bias ? vload(static_cast<const T*>(p.bias) + c0) : vzero();
-
-    // row[q]: the pool row of entry b0 + q, or -1 for a padding (any
-    // negative) or out-of-pool index; in_batch[q]: the entry exists
-    int32_t row[BPL];
-    bool in_batch[BPL];
-    u32x4 xv[BPL], sv[BPL][NV];
-#pragma unroll
-    for (int q = 0; q < BPL; ++q) {
-        in_batch[q] = b0 + q < nb;
-        const uint32_t b = in_batch[q] ? b0 + q : 0;
-        int32_t r = (int32_t)b;
-        if (p.conv_state_indices != nullptr) {
-            r = UB ? ld_uniform(p.conv_state_indices + b) : p.conv_state_indices[b];
-            if (r < 0 || r >= p.state_rows) r = -1;
+    for (int j = 0; j < NSLOT; ++j) {
+        if (64 * j + 63 >= NSV) {  // compile-time after unrolling
+            const int32_t xi = min(max((int32_t)(64 * j + lane) - NSV, 0), nxv - 1);
+            xv[j] = vload(xr + xi * EPV);
         }
-        row[q] = r;
-        const uint32_t rr = r >= 0 ? (uint32_t)r : 0u;
-        xv[q] = vload(static_cast<const T*>(p.x) + (size_t)b * p.x_stride[0] + c0);
-        const T* sp = static_cast<const T*>(p.conv_state) + (size_t)rr * p.conv_state_stride[0] + (size_t)c0 * H;
-#pragma unroll
-        for (int n = 0; n < NV; ++n) sv[q][n] = vload(sp + n * EPV);
     }
+    // this lane's channels: weights (CPL * W elements, XD * W dwords) and bias (XD dwords)
+    const uint32_t cl = c0 + CPL * lane;
+    const uint32_t cw = cl < a.dim ? cl : 0;
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(a.weight + (size_t)cw * W);
+    uint32_t wd[XD * W];
 #pragma unroll
-    for (int q = 0; q < BPL; ++q) {
-        float o[EPV];
-        float ns[EPV * H];
+    for (int k = 0; k < XD * W; ++k) wd[k] = wp[k];
+    uint32_t bd[XD];
 #pragma unroll
-        for (int e = 0; e < EPV; ++e) {
+    for (int k = 0; k < XD; ++k) bd[k] = HAS_BIAS ? reinterpret_cast<const uint32_t*>(a.bias + cw)[k] : 0u;
+    // the pool index (a scalar load) after the index-free loads, which are
+    // then all in flight while the state addresses wait for it; the
+    // scheduling fence keeps the compiler from hoisting the index load and
+    // its wait above them
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t row = (int32_t)b;
+    if constexpr (HAS_IDX) {
+        row = ld_uniform(a.idx + b);
+        if (row < 0 || row >= a.state_rows) row = -1;  // padding (any negative) or out of the pool
+    }
+    // state vectors, also unconditional (a padding entry reads row 0, lanes
+    // past the state part an in-bounds vector; both are dropped)
+    T* sp = a.conv_state + (size_t)(row >= 0 ? row : 0) * a.state_row + (size_t)c0 * H;
+#pragma unroll
+    for (int j = 0; j < NSLOT; ++j) {
+        const int32_t vi = 64 * j + lane;
+        u32x4 v = vzero();
+        if (64 * j < NSV) v = vload(sp + min(vi, nsv - 1) * EPV);
+        if (64 * j + 63 >= NSV) v = vi >= NSV ? xv[j] : v;
+        seg[64 * j + lane] = v;
+    }
+    __builtin_amdgcn_wave_barrier();
+    uint32_t* sd = reinterpret_cast<uint32_t*>(seg);
+    uint32_t st[SD], xd[XD];
+#pragma unroll
+    for (int i = 0; i < SD; ++i) st[i] = sd[SD * lane + i];
+#pragma unroll
+    for (int i = 0; i < XD; ++i) xd[i] = sd[4 * NSV + XD * lane + i];
+    // element n of a dword array: half (n & 1) of dword n / 2 (16-bit) or dword n (fp32)
+    auto elem = [&](const uint32_t* d, int n) -> uint32_t {
+        if constexpr (EPV == 4) return d[n];
+        else return (n & 1) ? (d[n >> 1] >> 16) : (d[n >> 1] & 0xffffu);
+    };
+    auto as_f32 = [&](uint32_t bits) -> float {
+        if constexpr (EPV == 4) return __uint_as_float(bits);
+        else return to_f32(T{(uint16_t)bits});
+    };
+    uint32_t nd[SD], od[XD];
+    {
+        uint32_t sraw[CPL * H], nraw[CPL * H];
+#pragma unroll
+        for (int n = 0; n < CPL * H; ++n) sraw[n] = elem(st, n);
+        float o[CPL];
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+            const uint32_t xb = elem(xd, e);
             float win[W], w[W];
 #pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const int n = e * H + i;
-                win[i] = vget<T>(sv[q][n / EPV], n % EPV);
-            }
-            win[H] = vget<T>(xv[q], e);
+            for (int i = 0; i < H; ++i) win[i] = as_f32(sraw[e * H + i]);
+            win[H] = as_f32(xb);
 #pragma unroll
-            for (int k = 0; k < W; ++k) {
-                const int n = e * W + k;
-                w[k] = vget<T>(wv[n / EPV], n % EPV);
-            }
-            float acc = conv_taps<W>(vget<T>(bv, e), w, win);
+            for (int k = 0; k < W; ++k) w[k] = as_f32(elem(wd, e * W + k));
+            const float bias = HAS_BIAS ? as_f32(elem(bd, e)) : 0.0f;
+            float acc = conv_taps<W>(bias, w, win);
             if constexpr (SILU) acc = silu(acc);
             o[e] = acc;
 #pragma unroll
-            for (int i = 0; i < H; ++i) ns[e * H + i] = win[i + 1];
+            for (int i = 0; i < H; ++i) nraw[e * H + i] = i + 1 < H ? sraw[e * H + i + 1] : xb;
         }
-        if (!in_batch[q]) continue;
-        T* op = static_cast<T*>(p.out) + (size_t)(b0 + q) * p.out_stride[0] + c0;
-        if (row[q] < 0) {  // padding (or out-of-pool) entry: zero output, state untouched
-            vstore(op, vzero());
-            continue;
-        }
-        vstore(op, vpack<T>(o));
-        T* sp = static_cast<T*>(p.conv_state) + (size_t)row[q] * p.conv_state_stride[0] + (size_t)c0 * H;
+        if constexpr (EPV == 4) {
 #pragma unroll
-        for (int n = 0; n < NV; ++n) vstore(sp + n * EPV, vpack<T>(ns + n * EPV));
+            for (int i = 0; i < SD; ++i) nd[i] = nraw[i];
+#pragma unroll
+            for (int i = 0; i < XD; ++i) od[i] = __float_as_uint(o[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < SD; ++i) nd[i] = nraw[2 * i] | (nraw[2 * i + 1] << 16);
+#pragma unroll
+            for (int i = 0; i < XD; ++i) od[i] = pack2<T>(o[2 * i], o[2 * i + 1]);
+        }
+        if (row < 0) {  // padding entry: zero output, state untouched
+#pragma unroll
+            for (int i = 0; i < XD; ++i) od[i] = 0u;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < SD; ++i) sd[SD * lane + i] = nd[i];
+#pragma unroll
+    for (int i = 0; i < XD; ++i) sd[4 * NSV + XD * lane + i] = od[i];
+    __builtin_amdgcn_wave_barrier();
+    T* orow = a.out + (size_t)b * a.out_row + c0;
+#pragma unroll
+    for (int j = 0; j < NSLOT; ++j) {
+        const int32_t vi = 64 * j + lane;
+        if (vi >= NTV) continue;
+        const u32x4 r = seg[vi];
+        if (vi < NSV) {
+            if (row >= 0 && vi < nsv) vstore(sp + vi * EPV, r);
+        } else if (vi - NSV < nxv) {
+            vstore(orow + (vi - NSV) * EPV, r);
+        }
     }
 }
 
@@ -421,8 +501,12 @@ __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
 
 namespace {
 
+// update_lin: 16-byte vectors per lane (each wavefront covers 16 * EPV * kLinNV
+// channels). C4a (256 x 5120 bf16, W4): 1 -> 7.58 us, 2 -> 7.12 us, 4 -> 7.50 us.
+constexpr int kLinNV = 2;
+
 template <typename T>
-bool vec1_ok(const cc1d_update_params& p) {
+bool lin_ok(const cc1d_update_params& p) {
     constexpr int64_t EPV = elems16<T>::value;
     const int64_t H = p.width - 1;
     if (p.cache_seqlens != nullptr || p.seqlen != 1 || p.state_len != H) return false;
@@ -431,10 +515,15 @@ bool vec1_ok(const cc1d_update_params& p) {
     if (p.x_stride[0] % EPV || p.out_stride[0] % EPV) return false;
     if (p.conv_state_stride[2] != 1 || p.conv_state_stride[1] != H || p.conv_state_stride[0] % EPV) return false;
     if (p.weight_stride[1] != 1 || p.weight_stride[0] != p.width) return false;
-    if (p.bias != nullptr && (p.bias_stride != 1 || !aligned16(p.bias))) return false;
-    if (!aligned16(p.x) || !aligned16(p.out) || !aligned16(p.conv_state) || !aligned16(p.weight)) return false;
-    // 32-bit lane indices; size_t offsets
-    if (p.batch * p.dim >= ((int64_t)1 << 31) || p.state_rows >= ((int64_t)1 << 31)) return false;
+    if (p.bias != nullptr && (p.bias_stride != 1 || (reinterpret_cast<uintptr_t>(p.bias) & 3u))) return false;
+    if (!aligned16(p.x) || !aligned16(p.out) || !aligned16(p.conv_state) ||
+        (reinterpret_cast<uintptr_t>(p.weight) & 3u))
+        return false;
+    // 32-bit channel indices and row strides, a grid of (groups, batch) blocks; size_t offsets
+    const int64_t lim = (int64_t)1 << 31;
+    if (p.dim >= lim || p.batch > 65535 || p.state_rows >= lim) return false;
+    if (p.x_stride[0] >= lim || p.out_stride[0] >= lim || p.conv_state_stride[0] >= lim) return false;
+    if (p.x_stride[0] < 0 || p.out_stride[0] < 0 || p.conv_state_stride[0] < 0) return false;
     return true;
 }
 
@@ -474,15 +563,28 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                 constexpr bool SILU = decltype(sc)::value;
                 UpdArgs a;
                 a.p = p;
-                a.ngroups = 0;
-                if (vec1_ok<T>(p)) {
-                    constexpr int BPL = 2;
-                    a.ngroups = p.dim / EPV;
-                    a.n_items = ceil_div(p.batch, BPL) * a.ngroups;
-                    return with_flag(a.ngroups % 64 == 0, [&](auto ub) {
-                        update_vec1<T, W, SILU, BPL, decltype(ub)::value>
-                            <<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
-                        return launch_status();
+                if (lin_ok<T>(p)) {
+                    LinArgs<T> la;
+                    la.x = static_cast<const T*>(p.x);
+                    la.weight = static_cast<const T*>(p.weight);
+                    la.bias = static_cast<const T*>(p.bias);
+                    la.conv_state = static_cast<T*>(p.conv_state);
+                    la.idx = p.conv_state_indices;
+                    la.out = static_cast<T*>(p.out);
+                    la.x_row = (uint32_t)p.x_stride[0];
+                    la.out_row = (uint32_t)p.out_stride[0];
+                    la.state_row = (uint32_t)p.conv_state_stride[0];
+                    la.dim = (uint32_t)p.dim;
+                    la.state_rows = (int32_t)p.state_rows;
+                    la.unused = 0;
+                    // grid: channel groups x batch entries (no division in the kernel)
+                    const dim3 grid((unsigned)ceil_div(p.dim, 16 * EPV * kLinNV), (unsigned)p.batch);
+                    return with_flag(p.bias != nullptr, [&](auto hb) {
+                        return with_flag(p.conv_state_indices != nullptr, [&](auto hi) {
+                            update_lin<T, W, kLinNV, SILU, decltype(hb)::value, decltype(hi)::value>
+                                <<<grid, 64, 0, stream>>>(la);
+                            return launch_status();
+                        });
                     });
                 }
                 a.n_items = p.batch * p.dim;
