@@ -13,8 +13,8 @@
 // cc1d_bwd adds the sums into the caller's zeroed fp32 accumulators with
 // atomics -- as in the reference, the order of those adds (over batches and
 // segments) is not fixed. cc1d_bwd_typed writes them as partial records
-// instead, and bwd_reduce adds each channel's records in a fixed order and
-// rounds once to the dtype.
+// instead, and bwd_reduce adds each channel's records in a fixed order
+// (several records in flight per wavefront) and rounds once to the dtype.
 //
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
@@ -1049,8 +1049,15 @@ int launch_plan(BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream) {
 }
 
 // Sum of the partial records of each channel, in a fixed order, written in
-// the dtype: one block per 64 channels; the 16 wavefronts of a block take
-// every 16th record of the channel and are summed through LDS.
+// the dtype. Lanes run along the values of a record, so every load of a
+// wavefront reads 64 consecutive floats: value o of the outputs is (channel
+// o / (W+1), tap o % (W+1), the bias as tap W) for row and generic records,
+// whose (W+1) values per channel are contiguous, and value f of a channel
+// group's record (NC x W taps, then NC biases) for channel-last records.
+// Wavefront q of a block takes records q, q + waves, ... in that order, RB of
+// them in flight at a time, and the block adds its wavefronts' sums in LDS in
+// wavefront order. (With a lane per channel reading values 16-20 bytes
+// apart, C3's 10.5 MB of records took 8-10 us.)
 struct RedArgs {
     const float* part;
     void* dweight;
@@ -1058,50 +1065,62 @@ struct RedArgs {
     int64_t dweight_stride[2];
     int64_t dbias_stride;
     int64_t batch, dim, nseg, groups;
-    int kind;
-    int nc;  // cl: channels per record
+    int nc;           // cl: channels per record
+    int64_t nout;     // values reduced: dim * (W+1) (rows, generic) or groups * nc * (W+1) (cl)
 };
 
-template <typename T, int W>
+template <typename T, int W, int KIND>
 __global__ void __launch_bounds__(1024) bwd_reduce(const RedArgs r) {
-    constexpr int SPLIT = 16;
-    __shared__ float acc[SPLIT][W + 1][64];
-    const int ci = threadIdx.x & 63;
-    const int sp = threadIdx.x >> 6;
-    const int64_t c = (int64_t)blockIdx.x * 64 + ci;
-    float s[W + 1];
+    constexpr int RB = 8;  // records in flight per wavefront
+    __shared__ float acc[16][64];
+    const int lane = threadIdx.x & 63;
+    const int q = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int64_t o = (int64_t)blockIdx.x * 64 + lane;  // output value of this lane
+    const int64_t n = r.batch * r.nseg;                  // records per channel
+    const bool on = o < r.nout;
+    // channel, tap (W: bias) and the offset of this value in record j = (b, g)
+    int64_t c, k, grp = 0, f = 0;
+    if constexpr (KIND == kBwdCl) {
+        const int64_t rec = (int64_t)r.nc * (W + 1);
+        grp = o / rec;
+        f = o - grp * rec;
+        const bool tap = f < (int64_t)r.nc * W;
+        c = grp * r.nc + (tap ? f / W : f - (int64_t)r.nc * W);
+        k = tap ? f % W : W;
+    } else {
+        c = o / (W + 1);
+        k = o - c * (W + 1);
+    }
+    auto at = [&](int64_t j) -> const float* {
+        const int64_t b = j / r.nseg, g = j - b * r.nseg;
+        if constexpr (KIND == kBwdCl)
+            return r.part + ((b * r.nseg + g) * r.groups + grp) * (int64_t)r.nc * (W + 1) + f;
+        else if constexpr (KIND == kBwdRows)
+            return r.part + ((b * r.dim + c) * r.nseg + g) * (W + 1) + k;
+        else
+            return r.part + ((b * r.nseg + g) * r.dim + c) * (W + 1) + k;
+    };
+    float sum = 0.0f;
+    if (on) {
+        for (int64_t jb = q; jb < n; jb += (int64_t)nw * RB) {
+            float v[RB];
 #pragma unroll
-    for (int k = 0; k <= W; ++k) s[k] = 0.0f;
-    if (c < r.dim) {
-        const int64_t n = r.batch * r.nseg;  // records per channel
-        for (int64_t j = sp; j < n; j += SPLIT) {
-            const int64_t b = j / r.nseg, q = j - b * r.nseg;
-            if (r.kind == kBwdCl) {
-                const int64_t g = c / r.nc, cc = c - g * r.nc;
-                const float* rec = r.part + ((b * r.nseg + q) * r.groups + g) * (int64_t)r.nc * (W + 1);
-#pragma unroll
-                for (int k = 0; k < W; ++k) s[k] += rec[cc * W + k];
-                s[W] += rec[(int64_t)r.nc * W + cc];
-            } else {
-                const int64_t item = r.kind == kBwdRows ? (b * r.dim + c) * r.nseg + q : (b * r.nseg + q) * r.dim + c;
-                const float* rec = r.part + item * (W + 1);
-#pragma unroll
-                for (int k = 0; k <= W; ++k) s[k] += rec[k];
+            for (int u = 0; u < RB; ++u) {
+                const int64_t j = jb + (int64_t)u * nw;
+                v[u] = j < n ? *at(j) : 0.0f;
             }
+#pragma unroll
+            for (int u = 0; u < RB; ++u) sum += v[u];
         }
     }
-#pragma unroll
-    for (int k = 0; k <= W; ++k) acc[sp][k][ci] = s[k];
+    acc[q][lane] = sum;
     __syncthreads();
-    if (sp == 0 && c < r.dim) {
-#pragma unroll
-        for (int k = 0; k <= W; ++k) {
-            float t = 0.0f;
-#pragma unroll
-            for (int q = 0; q < SPLIT; ++q) t += acc[q][k][ci];
-            if (k < W) st(static_cast<T*>(r.dweight), c * r.dweight_stride[0] + k * r.dweight_stride[1], t);
-            else if (r.dbias != nullptr) st(static_cast<T*>(r.dbias), c * r.dbias_stride, t);
-        }
+    if (q == 0 && on && c < r.dim) {
+        float t = 0.0f;
+        for (int w = 0; w < nw; ++w) t += acc[w][lane];
+        if (k < W) st(static_cast<T*>(r.dweight), c * r.dweight_stride[0] + k * r.dweight_stride[1], t);
+        else if (r.dbias != nullptr) st(static_cast<T*>(r.dbias), c * r.dbias_stride, t);
     }
 }
 
@@ -1212,9 +1231,14 @@ int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStrea
                 r.dim = p.dim;
                 r.nseg = pl.a.nseg;
                 r.groups = pl.a.groups;
-                r.kind = pl.kind;
                 r.nc = 64 * (pl.cpl > 0 ? pl.cpl : 1);
-                bwd_reduce<T, W><<<dim3((unsigned)ceil_div(p.dim, 64)), 1024, 0, stream>>>(r);
+                r.nout = pl.kind == kBwdCl ? pl.a.groups * r.nc * (W + 1) : p.dim * (W + 1);
+                const int64_t n = p.batch * pl.a.nseg;  // records per channel
+                const dim3 grid((unsigned)ceil_div(r.nout, 64));
+                const unsigned threads = 64 * (unsigned)(n < 16 ? n : 16);
+                if (pl.kind == kBwdRows) bwd_reduce<T, W, kBwdRows><<<grid, threads, 0, stream>>>(r);
+                else if (pl.kind == kBwdCl) bwd_reduce<T, W, kBwdCl><<<grid, threads, 0, stream>>>(r);
+                else bwd_reduce<T, W, kBwdGeneric><<<grid, threads, 0, stream>>>(r);
                 return launch_status();
             });
         });
