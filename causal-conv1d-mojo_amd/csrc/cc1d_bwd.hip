@@ -19,8 +19,8 @@
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
 //                   fwd_rows_vec (one item per wavefront, 4 per block).
-//   bwd_cl       -- channel-last (unit channel stride); a lane owns 4 bytes of
-//                   adjacent channels, a wavefront a tile of time steps.
+//   bwd_clw      -- channel-last (unit channel stride); a lane owns 4 bytes of
+//                   adjacent channels, a wavefront walks a run of time steps.
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
 #include <mutex>
 
@@ -31,17 +31,18 @@ namespace cc1d {
 struct BwdArgs {
     cc1d_bwd_params p;
     float* part;      // non-null: write weight/bias-gradient partial sums here instead of atomics
-    int64_t nseg;     // rows_vec: segments per row; cl: tile groups per row; generic: chunks per row
+    int64_t nseg;     // rows_vec: segments per row; cl: run groups per row; generic: chunks per row
     int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
-    int64_t chunk;    // cl: time steps per tile; generic: time steps per thread
+    int64_t chunk;    // cl: time steps per run; generic: time steps per thread
     int64_t groups;   // cl: channel groups of 64 * CPL
 };
 
 // channel-first rows: (row, segment) items per block, one per wavefront
 constexpr int kRowsWPB = 4;
-// channel-last launch shape: time steps per wavefront tile, tiles per block
-constexpr int kClTS = 16;
-constexpr int kClWPB = 4;
+// channel-last walk: time steps per chunk, per wavefront run, runs per block
+constexpr int kClG = 4;
+constexpr int kClR = 128;
+constexpr int kClWPB = 8;
 
 // Registers of one wavefront-segment of a row: VPT 16-byte vectors of x and
 // dout per lane, plus the halos (lane 0: the vector of x before the segment;
@@ -478,30 +479,33 @@ __device__ __forceinline__ void bwd_chunk(const cc1d_bwd_params& p, int64_t b, i
     }
 }
 
-// ---- channel-last (unit channel stride) backward, tiled ----------------
+// ---- channel-last (unit channel stride) backward: a walk along time ------
 //
-// A lane owns CPL adjacent channels and a wavefront one tile of TS time
-// steps of 64 * CPL channels. The tile's registers hold x rows
-// t0-W+1 .. t0+TS+W-2 and dout rows t0 .. t0+TS+W-2; dpre is recomputed for
-// t0 .. t0+TS+W-2 (the last W-1 belong to the next tile and only feed dx
-// here). Index arithmetic is 32-bit inside a batch (the launcher checks the
-// ranges).
-
-template <typename T, int W, int CPL, int TS> struct ClTile {
-    static constexpr int H = W - 1;
-    static constexpr int NX = TS + 2 * H;  // x rows: position t0 - H + i
-    static constexpr int ND = TS + H;      // dout / dpre rows: position t0 + j
-    Lanes<T, CPL> xv[NX], gv[ND];
-};
-
-template <int W, int CPL> struct ClPartials {
-    float pw[W][CPL];
-    float pb[CPL];
-};
+// A lane owns CPL adjacent channels (4 bytes) and a wavefront the 64 * CPL
+// channels of one run of R time steps [t0, t0 + R). The wavefront walks its
+// run in chunks of G steps, one 256-byte row of x and of dout per load
+// instruction, the next chunk's loads in flight while the current chunk is
+// computed. x and dpre of the last H = W - 1 positions slide in registers;
+// dx of position s is emitted once dpre[s + H] is known, so a run computes
+// dpre for [t0, t0 + R + H) (a tail of H steps, the next run's first) and
+// emits dx for [t0, t0 + R). Loads are unconditional at positions clamped
+// into [0, L); a chunk whose window lies inside the sequence with one
+// seq_idx id (>= 0) takes the ungated arithmetic, any other chunk the same
+// steps with every condition applied (all of them wave-uniform: one time
+// step per instruction row, the ids in scalar registers). Index arithmetic
+// is 32-bit inside a batch (the launcher checks the ranges).
+//
+// Launch shape (C3, 8192 x 4096 bf16): chunks of 4 steps, runs of 128, 8
+// runs per block -- 2048 wavefronts, two per SIMD. Measured against it
+// (same box, us for seq_idx / initial_states): tiles of 16 steps loaded at
+// once, 4 per block, 46.3 / 45.0 (the previous kernel); runs of 64 or 96
+// steps 48-49; runs of 192 52-57; chunks of 8 steps 46-48; 4 runs per block
+// 44.0 / 42.0; 8 runs per block 42.1 / 41.0. A copy with the same access
+// pattern and no arithmetic takes 36.8 us.
 
 // The weights and bias of a lane's channels, kept raw: they are read before
-// the tile and converted where they are used, so no conversion waits for
-// them (memory counters retire in order) ahead of the tile's loads.
+// the walk and converted where they are used, so no conversion waits for
+// them (memory counters retire in order) ahead of the first chunk's loads.
 // Without a bias the bias read goes to x's first element (an unconditional
 // load, so no branch waits on it) and bias() returns zero.
 template <typename T, int W, int CPL> struct ClWeights {
@@ -522,353 +526,385 @@ template <typename T, int W, int CPL> struct ClWeights {
     __device__ __forceinline__ float bias(int e) const { return has_bias ? to_f32(b[e]) : 0.0f; }
 };
 
-// Issue the loads of the tile at t0 (rows outside the sequence are zero;
-// rows before 0 come from initial_states when given).
-template <typename T, int W, int CPL, int TS>
-__device__ __forceinline__ void cl_bwd_load(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0, bool active,
-                                            ClTile<T, W, CPL, TS>& r) {
-    using Tile = ClTile<T, W, CPL, TS>;
-    constexpr int H = W - 1;
-    const int32_t L = (int32_t)p.seqlen;
-    const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
-    // lanes past the last channel read channel 0 (in bounds) so that every
-    // condition below is wave-uniform; they store nothing and their
-    // partials are dropped
-    const int32_t cr = active ? c0 : 0;
-    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + cr;
-    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + cr;
-    if (t0 >= H && t0 + TS + H <= L) {  // every row of the tile lies inside [0, L)
+// G rows of x and dout from position c0 on, raw; ids[i]: seq_idx at position
+// c0 - H + i (clamped into [0, L)), read through the scalar cache (NI = G + H
+// with seq_idx, else 1 unused).
+template <typename T, int CPL, int G, int NI> struct ClChunk {
+    Lanes<T, CPL> x[G], g[G];
+    int32_t ids[NI];
+};
+
+// Sliding state of a walk: x and dpre at the H positions before the current
+// one (x zero before the sequence or initial_states there, dpre zero before
+// the run), and the weight/bias-gradient partial sums.
+template <int W, int CPL> struct ClWalk {
+    float xw[W - 1][CPL], dw[W - 1][CPL];
+    float pw[W][CPL], pb[CPL];
+    // Ends a step's partial-sum updates where they are written: otherwise the
+    // compiler sinks each running sum's fma towards its next use (the next
+    // step's), until a chunk's updates all sit at its end and every step's
+    // dpre and x stay live until then.
+    __device__ __forceinline__ void pin_sums() {
 #pragma unroll
-        for (int i = 0; i < Tile::NX; ++i) r.xv[i].template load<false>(xb + (t0 - H + i) * xs2);
+        for (int e = 0; e < CPL; ++e) {
 #pragma unroll
-        for (int j = 0; j < Tile::ND; ++j) r.gv[j].template load<false>(gb + (t0 + j) * gs2);
-    } else {
-#pragma unroll
-        for (int i = 0; i < Tile::NX; ++i) {
-            const int32_t s = t0 - H + i;
-            r.xv[i].zero();
-            if (s >= 0 && s < L) r.xv[i].template load<false>(xb + s * xs2);
-        }
-#pragma unroll
-        for (int j = 0; j < Tile::ND; ++j) {
-            const int32_t t = t0 + j;
-            r.gv[j].zero();
-            if (t < L) r.gv[j].template load<false>(gb + t * gs2);
+            for (int k = 0; k < W; ++k) asm volatile("" : "+v"(pw[k][e]));
+            asm volatile("" : "+v"(pb[e]));
         }
     }
-    if (p.initial_states != nullptr && t0 < H && active) {
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-            const int32_t s = t0 - H + i;
-            if (s < 0) {
-                float f[CPL];
-#pragma unroll
-                for (int e = 0; e < CPL; ++e)
-                    f[e] = ld(static_cast<const T*>(p.initial_states),
-                              b * p.initial_states_stride[0] + (c0 + e) * p.initial_states_stride[1] +
-                                  (s + H) * p.initial_states_stride[2]);
-                r.xv[i].set(f);
-            }
-        }
-    }
+};
+
+// One dword of a row at byte offset off from the wavefront-uniform base
+// (offsets below 2^32: the launcher checks the ranges). A 64-bit uniform base
+// plus a 32-bit per-lane offset is the scalar-base form of the global
+// access (global_load_dword v, v_off, s[base]): one 32-bit add per access.
+template <typename T, int CPL> __device__ __forceinline__ Lanes<T, CPL> row_load(const T* base, uint32_t off) {
+    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
+    Lanes<T, CPL> v;
+    v.d[0] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(base) + off);
+    return v;
+}
+template <typename T, int CPL> __device__ __forceinline__ void row_store_nt(T* base, uint32_t off, const Lanes<T, CPL>& v) {
+    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
+    __builtin_nontemporal_store(v.d[0], reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(base) + off));
 }
 
-// seq_idx of the tile's x-row window: lane i < NX reads position t0 - H + i
-// at a clamped address, so the reads are one unconditional vector load (no
-// wait until the value is used). A position outside [0, L) carries the id
-// of the nearest position inside; the terms it gates are zero either way
-// (x rows there are zero, dpre rows past the end are zero).
-template <int NX>
-__device__ __forceinline__ int32_t cl_window_id(const int32_t* sr, int32_t ss1, int32_t L, int32_t t0, int32_t H,
-                                                int lane) {
-    static_assert(NX <= 64, "the id window must fit in one wavefront");
-    const int32_t s = t0 - H + lane;
-    return sr[(s < 0 ? 0 : (s < L ? s : L - 1)) * ss1];
+// A copy of a lane's raw row that the compiler cannot see through: the
+// widening of a row is then done in the step that uses it, not for a whole
+// chunk at once (which kept twice the chunk's registers live).
+template <typename T, int CPL> __device__ __forceinline__ Lanes<T, CPL> pinned(Lanes<T, CPL> v) {
+    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
+    asm volatile("" : "+v"(v.d[0]));
+    return v;
 }
 
-// dpre, dx (+ dfinal tail, dinitial_states) and the weight/bias-gradient
-// partials of a loaded tile whose rows belong to one sequence.
-template <typename T, int W, int CPL, int TS, bool SILU>
-__device__ __forceinline__ void cl_bwd_compute(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
-                                               bool active, const ClTile<T, W, CPL, TS>& r,
-                                               const ClWeights<T, W, CPL>& wt, ClPartials<W, CPL>& out) {
-    using Tile = ClTile<T, W, CPL, TS>;
-    constexpr int H = W - 1;
-    constexpr int ND = Tile::ND;
-    const int32_t L = (int32_t)p.seqlen;
-    const int32_t ds2 = (int32_t)p.dx_stride[2];
-    T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
-
-    float w[W][CPL], wq[W][CPL], bq[CPL];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-            w[k][e] = to_f32(wt.w[k][e]);
-            wq[k][e] = -kLog2e * w[k][e];
-        }
-        bq[e] = -kLog2e * wt.bias(e);
-    }
-
-    float dp[ND][CPL];
-#pragma unroll
-    for (int j = 0; j < ND; ++j) {
-        const int32_t t = t0 + j;
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            const float gval = r.gv[j].get(e);
-            float d = gval;
-            if constexpr (SILU) {
-                float q = bq[e];
-#pragma unroll
-                for (int k = 0; k < W; ++k) q = __builtin_fmaf(wq[k][e], r.xv[j + k].get(e), q);
-                d = silu_bwd_q(gval, q);
-            }
-            if (t >= L) d = 0.0f;
-            dp[j][e] = d;
-            if (j < TS) {
-                out.pb[e] += d;
-#pragma unroll
-                for (int k = 0; k < W; ++k) out.pw[k][e] = __builtin_fmaf(d, r.xv[j + k].get(e), out.pw[k][e]);
-            }
-        }
-    }
-    const int32_t m = H < L ? H : L;  // dfinal tail length
-#pragma unroll
-    for (int j = 0; j < TS; ++j) {
-        const int32_t t = t0 + j;
-        float o[CPL];
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[H - k][e], dp[j + k][e], acc);
-            o[e] = acc;
-        }
-        if (p.dfinal_states != nullptr && t >= L - m && t < L && active) {
-#pragma unroll
-            for (int e = 0; e < CPL; ++e)
-                o[e] = round_to<T>(o[e]) + ld(static_cast<const T*>(p.dfinal_states),
-                                              b * p.dfinal_states_stride[0] + (c0 + e) * p.dfinal_states_stride[1] +
-                                                  (t - L + H) * p.dfinal_states_stride[2]);
-        }
-        if (active && t < L) {
-            Lanes<T, CPL> ov;
-            ov.set(o);
-            ov.template store<true>(dxb + t * ds2);
-        }
-    }
-    // dinitial_states (bwd_full_cpu/kernel.mojo:210-219)
-    if (p.dinitial_states != nullptr && t0 == 0 && active) {
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
-                    (c0 + e) * p.dinitial_states_stride[1];
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], dp[i - k][e], acc);
-                st(di, i * p.dinitial_states_stride[2], acc);
-            }
-        }
-    }
-}
-
-// A tile whose window holds a seq_idx boundary: the same arithmetic with the
-// equality gate, time step after time step in a rolled loop over batches of
-// G steps. x and dout rows are read again (the tile's own loads have just
-// brought them into the cache), one batch of loads per iteration, used in
-// place; the last W rows of x, dpre and their ids slide in registers.
-// Unrolled over the tile's registers instead, the gated arithmetic took ~40
-// more VGPRs than the ungated one, and because both live in one kernel,
-// every tile ran at the lower occupancy. seq_idx
-// excludes initial_states, dfinal_states and dinitial_states (the entry
-// points reject the combination), so none of them appears here.
-template <typename T, int W, int CPL, int TS, bool SILU>
-__device__ __forceinline__ void cl_bwd_gated(const cc1d_bwd_params& p, uint32_t b, int32_t t0, int32_t c0,
-                                             bool active, int32_t lid, const ClWeights<T, W, CPL>& wt,
-                                             ClPartials<W, CPL>& out) {
-    constexpr int H = W - 1;
-    constexpr int NROW = TS + H;  // dpre rows t0 .. t0+TS+H-1
-    constexpr int G = 4;          // rows per batch of loads
-    const int32_t L = (int32_t)p.seqlen;
-    const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
-    const int32_t ds2 = (int32_t)p.dx_stride[2];
-    const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + c0;
-    const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c0;
-    T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c0;
-
-    float w[W][CPL], wq[W][CPL], bq[CPL];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-        for (int k = 0; k < W; ++k) {
-            w[k][e] = to_f32(wt.w[k][e]);
-            wq[k][e] = -kLog2e * w[k][e];
-        }
-        bq[e] = -kLog2e * wt.bias(e);
-    }
-
-    // x row s (and dout row s), zero outside [0, L)
-    auto load_x = [&](int32_t s, Lanes<T, CPL>& xr) {
-        xr.zero();
-        if (active && s >= 0 && s < L) xr.template load<false>(xb + s * xs2);
-    };
-    auto load_row = [&](int32_t s, Lanes<T, CPL>& xr, Lanes<T, CPL>& gr) {
-        load_x(s, xr);
-        gr.zero();
-        if (active && s < L) gr.template load<false>(gb + s * gs2);
-    };
-    float xw[W][CPL], dw[W][CPL];  // x and dpre at positions t-H .. t
-    int32_t iw[W];                 // their ids
-#pragma unroll
-    for (int k = 0; k < H; ++k) {
-        Lanes<T, CPL> xr;
-        load_x(t0 - H + k, xr);
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            xw[k + 1][e] = xr.get(e);
-            dw[k + 1][e] = 0.0f;
-        }
-        iw[k + 1] = __builtin_amdgcn_readlane(lid, k);
-    }
-    // one time step: x row t and dout row t enter the windows
-    auto step = [&](int j, const Lanes<T, CPL>& xr, const Lanes<T, CPL>& gr) {
-        const int32_t t = t0 + j;
-#pragma unroll
-        for (int k = 0; k < H; ++k) {
-            iw[k] = iw[k + 1];
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                xw[k][e] = xw[k + 1][e];
-                dw[k][e] = dw[k + 1][e];
-            }
-        }
-        iw[H] = __builtin_amdgcn_readlane(lid, j + H);
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) xw[H][e] = xr.get(e);
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            const float gval = gr.get(e);
-            float d = gval;
-            if constexpr (SILU) {
-                float q = bq[e];
-#pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (iw[k] == iw[H]) q = __builtin_fmaf(wq[k][e], xw[k][e], q);
-                d = silu_bwd_q(gval, q);
-            }
-            if (t >= L || iw[H] < 0) d = 0.0f;
-            dw[H][e] = d;
-            if (j < TS) {
-                out.pb[e] += d;
-#pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (iw[k] == iw[H]) out.pw[k][e] = __builtin_fmaf(d, xw[k][e], out.pw[k][e]);
-            }
-        }
-        // dx at position t - H: dpre rows t-H .. t, tap k kept when id(t-H+k) == id(t-H)
-        const int32_t s = t - H;
-        if (j >= H && active && s < L) {
-            float o[CPL];
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (iw[k] == iw[0]) acc = __builtin_fmaf(w[H - k][e], dw[k][e], acc);
-                o[e] = acc;
-            }
-            Lanes<T, CPL> ov;
-            ov.set(o);
-            ov.template store<true>(dxb + s * ds2);
-        }
-    };
-    // G rows per batch: their loads are issued together and used in place
-#pragma unroll 1
-    for (int j0 = 0; j0 < NROW; j0 += G) {
-        Lanes<T, CPL> xq[G], gq[G];
-#pragma unroll
-        for (int i = 0; i < G; ++i) load_row(t0 + j0 + i, xq[i], gq[i]);
-#pragma unroll
-        for (int i = 0; i < G; ++i)
-            if (j0 + i < NROW) step(j0 + i, xq[i], gq[i]);
-    }
-}
-
-// Kernel: the WPB wavefronts of a block take WPB consecutive tiles of the
-// same channels; their weight/bias-gradient partials are summed through LDS
-// and the block adds the sums with fp32 atomics on consecutive addresses.
-// Block order: channel group fastest, then tile group, then batch. With
-// seq_idx, a tile whose in-sequence rows all carry one id (>= 0) takes the
-// ungated path; rows outside [0, L) hold zeros (seq_idx excludes
-// initial_states) and feed only zeroed terms, so they do not count.
-template <typename T, int W, int CPL, int TS, int WPB, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(64 * WPB) bwd_cl(const BwdArgs a) {
-    using Tile = ClTile<T, W, CPL, TS>;
+// Kernel: the WPB wavefronts of a block take WPB consecutive runs of the same
+// channels; their weight/bias-gradient partials are summed through LDS and
+// the block adds the sums with fp32 atomics on consecutive addresses (or
+// writes them as its record). Block order: channel group fastest, then run
+// group, then batch.
+template <typename T, int W, int G, int R, int WPB, bool SILU, bool SEQ>
+__global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
+    constexpr int CPL = 4 / (int)sizeof(T);
     constexpr int H = W - 1;
     constexpr int NC = 64 * CPL;  // channels per wavefront
+    constexpr int NCH = R / G;    // chunks per run
+    static_assert(R == G || (R % (2 * G) == 0 && R >= 2 * G), "one chunk, or chunks in pairs");
+    static_assert(G >= H, "the first chunk covers the H steps whose dx belongs to the previous run");
+    using Chunk = ClChunk<T, CPL, G, SEQ ? G + H : 1>;
     __shared__ float red[WPB][NC * (W + 1)];
     const cc1d_bwd_params& p = a.p;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    // (the divisions run on the vector unit; uniform32 brings the results
+    // back to scalar registers, so every pointer derived from them is scalar)
     const uint32_t ngroups = (uint32_t)a.groups, ntgroups = (uint32_t)a.nseg;
-    const uint32_t g = blockIdx.x % ngroups;
-    const uint32_t rest = blockIdx.x / ngroups;
-    const uint32_t tg = rest % ntgroups;
-    const uint32_t b = rest / ntgroups;
+    const uint32_t grp = uniform32(blockIdx.x % ngroups);
+    const uint32_t rest = uniform32(blockIdx.x / ngroups);
+    const uint32_t tg = uniform32(rest % ntgroups);
+    const uint32_t b = uniform32(rest / ntgroups);
     const int32_t L = (int32_t)p.seqlen;
-    const int32_t t0 = (int32_t)uniform32((tg * WPB + wave) * TS);
-    const int32_t cw0 = (int32_t)(g * NC);
+    const int32_t t0 = (int32_t)uniform32((tg * WPB + wave) * R);
+    const int32_t cw0 = (int32_t)(grp * NC);
     const int32_t c0 = cw0 + lane * CPL;
     const bool active = c0 < (int32_t)p.dim;
 
-    ClPartials<W, CPL> part;
+    ClWalk<W, CPL> s;
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
-        part.pb[e] = 0.0f;
+        s.pb[e] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < W; ++k) part.pw[k][e] = 0.0f;
+        for (int k = 0; k < W; ++k) s.pw[k][e] = 0.0f;
     }
-    if (t0 < L) {  // tiles past the end only join the block reduction
-        // the window's ids (and the weights) are read before the tile: memory
-        // counters retire in order, so the branch on them waits for these
-        // loads only
-        int32_t lid = 0;
-        if constexpr (SEQ)
-            lid = cl_window_id<Tile::NX>(p.seq_idx + b * p.seq_idx_stride[0], (int32_t)p.seq_idx_stride[1], L, t0,
-                                         H, lane);
+    if (t0 < L) {  // runs past the end only join the block reduction
+        const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
+        const int32_t ds2 = (int32_t)p.dx_stride[2];
+        // lanes past the last channel read channel 0 of the group's rows (in
+        // bounds); they store nothing and their partials are dropped
+        const int32_t lo = active ? lane * CPL : 0;
+        const uint32_t lob = (uint32_t)lo * (uint32_t)sizeof(T);  // the lane's byte offset in a row
+        const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + cw0;
+        const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + cw0;
+        T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + cw0;
+        const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
+        const int32_t ss1 = SEQ ? (int32_t)p.seq_idx_stride[1] : 0;
+        auto clampL = [&](int32_t t) { return t < 0 ? 0 : (t < L ? t : L - 1); };
+
+        // loads of the rows of chunk c (NR of them) and of its id window
+        auto load = [&](int32_t cs, Chunk& ch, auto nr) {
+            constexpr int NR = decltype(nr)::value;
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                const int32_t t = clampL(cs + j);
+                ch.x[j] = row_load<T, CPL>(xb, (uint32_t)(t * xs2) * (uint32_t)sizeof(T) + lob);
+                ch.g[j] = row_load<T, CPL>(gb, (uint32_t)(t * gs2) * (uint32_t)sizeof(T) + lob);
+            }
+            if constexpr (SEQ) {
+#pragma unroll
+                for (int i = 0; i < G + H; ++i) ch.ids[i] = ld_uniform(sr + clampL(cs - H + i) * ss1);
+            }
+        };
+
+        // x rows t0-H .. t0-1 (zero before the sequence, or initial_states)
+        Lanes<T, CPL> prime[H];
+        const bool prime_rows = t0 >= H;
+        if (prime_rows) {
+#pragma unroll
+            for (int k = 0; k < H; ++k)
+                prime[k] = row_load<T, CPL>(xb, (uint32_t)((t0 - H + k) * xs2) * (uint32_t)sizeof(T) + lob);
+        }
         ClWeights<T, W, CPL> wt;
         wt.load(p, c0, active);
-        Tile r;
-        cl_bwd_load<T, W, CPL, TS>(p, b, t0, c0, active, r);
-        bool one_id = true;
-        if constexpr (SEQ) {
-            const int32_t s = t0 - H + lane;
-            const int32_t id_cur = __builtin_amdgcn_readlane(lid, H);
-            one_id = id_cur >= 0 && __ballot(lane < Tile::NX && s >= 0 && s < L && lid != id_cur) == 0;
+        Chunk A, B;
+        load(t0, A, std::integral_constant<int, G>{});
+
+        float w[W][CPL], bias[CPL];
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+#pragma unroll
+            for (int k = 0; k < W; ++k) w[k][e] = to_f32(wt.w[k][e]);
+            bias[e] = wt.bias(e);
         }
-        if (one_id) cl_bwd_compute<T, W, CPL, TS, SILU>(p, b, t0, c0, active, r, wt, part);
-        else if constexpr (SEQ) cl_bwd_gated<T, W, CPL, TS, SILU>(p, b, t0, c0, active, lid, wt, part);
+#pragma unroll
+        for (int k = 0; k < H; ++k) {
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                s.xw[k][e] = prime_rows ? prime[k].get(e) : 0.0f;
+                s.dw[k][e] = 0.0f;
+            }
+        }
+        if (!prime_rows && p.initial_states != nullptr && active) {  // t0 == 0
+            const int32_t cl = opaque(c0);
+#pragma unroll
+            for (int k = 0; k < H; ++k)
+#pragma unroll
+                for (int e = 0; e < CPL; ++e)
+                    s.xw[k][e] = ld(static_cast<const T*>(p.initial_states),
+                                    b * p.initial_states_stride[0] + (cl + e) * p.initial_states_stride[1] +
+                                        k * p.initial_states_stride[2]);
+        }
+        const int32_t m = H < L ? H : L;  // dfinal tail length
+
+        // shift the windows by one position: x and dpre of the current step enter
+        auto slide = [&](const float* xc, const float* dn) {
+#pragma unroll
+            for (int k = 0; k + 1 < H; ++k)
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) {
+                    s.xw[k][e] = s.xw[k + 1][e];
+                    s.dw[k][e] = s.dw[k + 1][e];
+                }
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                s.xw[H - 1][e] = xc[e];
+                s.dw[H - 1][e] = dn[e];
+            }
+        };
+        auto store_dx = [&](int32_t pos, const float* o) {
+            Lanes<T, CPL> ov;
+            ov.set(o);
+            row_store_nt<T, CPL>(dxb, (uint32_t)(pos * ds2) * (uint32_t)sizeof(T) + lob, ov);
+        };
+
+        // NS steps of chunk ch at cs, ungated (the chunk's window [cs-H, cs+NS+H)
+        // lies in [0, L) with one id); ACC: the steps are the run's own;
+        // HEAD: the run's first chunk (dx before the run belongs to the
+        // previous one)
+        auto steps_clean = [&](const Chunk& ch, int32_t cs, auto ns, auto accc, auto headc) {
+            constexpr int NS = decltype(ns)::value;
+            constexpr bool ACC = decltype(accc)::value;
+            constexpr bool HEAD = decltype(headc)::value;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                float xc[CPL], dn[CPL], o[CPL];
+                const Lanes<T, CPL> xl = pinned(ch.x[j]), gl = pinned(ch.g[j]);
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) {
+                    xc[e] = xl.get(e);
+                    const float gval = gl.get(e);
+                    float d = gval;
+                    if constexpr (SILU) {
+                        float pre = bias[e];
+#pragma unroll
+                        for (int k = 0; k < H; ++k) pre = __builtin_fmaf(w[k][e], s.xw[k][e], pre);
+                        pre = __builtin_fmaf(w[H][e], xc[e], pre);
+                        d = silu_bwd_q(gval, -kLog2e * pre);
+                    }
+                    dn[e] = d;
+                    if constexpr (ACC) {
+                        s.pb[e] += d;
+#pragma unroll
+                        for (int k = 0; k < H; ++k) s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
+                        s.pw[H][e] = __builtin_fmaf(d, xc[e], s.pw[H][e]);
+                    }
+                    // dx at position cs + j - H: dpre there .. here, taps w[H] .. w[0]
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < H; ++k) acc = __builtin_fmaf(w[H - k][e], s.dw[k][e], acc);
+                    o[e] = __builtin_fmaf(w[0][e], d, acc);
+                }
+                if (active && (j >= H || !HEAD)) store_dx(cs + j - H, o);
+                slide(xc, dn);
+                if constexpr (ACC) s.pin_sums();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // the same steps with every condition: positions past the end,
+        // seq_idx gates, dfinal_states, dinitial_states (chunk 0 of run 0)
+        auto steps_gated = [&](const Chunk& ch, int32_t cs, auto ns, auto accc) {
+            constexpr int NS = decltype(ns)::value;
+            constexpr bool ACC = decltype(accc)::value;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const int32_t pos = cs + j;
+                const bool in = pos < L;
+                int32_t idk[H], idp = 0;  // ids of the window positions and of pos
+                if constexpr (SEQ) {
+#pragma unroll
+                    for (int k = 0; k < H; ++k) idk[k] = ch.ids[j + k];
+                    idp = ch.ids[j + H];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < H; ++k) idk[k] = 0;
+                }
+                const bool dead = !in || idp < 0;
+                float xc[CPL], dn[CPL];
+                const Lanes<T, CPL> xl = pinned(ch.x[j]), gl = pinned(ch.g[j]);
+#pragma unroll
+                for (int e = 0; e < CPL; ++e) {
+                    xc[e] = in ? xl.get(e) : 0.0f;
+                    const float gval = gl.get(e);
+                    float d = gval;
+                    if constexpr (SILU) {
+                        float pre = bias[e];
+#pragma unroll
+                        for (int k = 0; k < H; ++k)
+                            if (idk[k] == idp) pre = __builtin_fmaf(w[k][e], s.xw[k][e], pre);
+                        pre = __builtin_fmaf(w[H][e], xc[e], pre);
+                        d = silu_bwd_q(gval, -kLog2e * pre);
+                    }
+                    if (dead) d = 0.0f;
+                    dn[e] = d;
+                    if constexpr (ACC) {
+                        s.pb[e] += d;
+#pragma unroll
+                        for (int k = 0; k < H; ++k)
+                            if (idk[k] == idp) s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
+                        s.pw[H][e] = __builtin_fmaf(d, xc[e], s.pw[H][e]);
+                    }
+                }
+                // dx at position sp = pos - H: tap k kept when id(sp + k) == id(sp)
+                const int32_t sp = pos - H;
+                if (sp >= t0 && sp < L && active) {
+                    float o[CPL];
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) {
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < H; ++k)
+                            if (idk[k] == idk[0]) acc = __builtin_fmaf(w[H - k][e], s.dw[k][e], acc);
+                        if (idp == idk[0]) acc = __builtin_fmaf(w[0][e], dn[e], acc);
+                        o[e] = acc;
+                    }
+                    if (p.dfinal_states != nullptr && sp >= L - m) {
+                        const int32_t cl = opaque(c0);
+#pragma unroll
+                        for (int e = 0; e < CPL; ++e)
+                            o[e] = round_to<T>(o[e]) + ld(static_cast<const T*>(p.dfinal_states),
+                                                          b * p.dfinal_states_stride[0] +
+                                                              (cl + e) * p.dfinal_states_stride[1] +
+                                                              (sp - L + H) * p.dfinal_states_stride[2]);
+                    }
+                    store_dx(sp, o);
+                }
+                slide(xc, dn);
+                if constexpr (ACC) s.pin_sums();
+                // dinitial_states (bwd_full_cpu/kernel.mojo:210-219): once the
+                // window holds dpre[0 .. H-1] (position H-1 is step H-1 of the
+                // chunk at 0, as chunks start at multiples of G >= H)
+                if (j == H - 1 && cs == 0 && p.dinitial_states != nullptr && active) {
+                    const int32_t cl = opaque(c0);
+#pragma unroll
+                    for (int e = 0; e < CPL; ++e) {
+                        T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
+                                (cl + e) * p.dinitial_states_stride[1];
+#pragma unroll
+                        for (int i = 0; i < H; ++i) {
+                            float acc = 0.0f;
+#pragma unroll
+                            for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], s.dw[i - k][e], acc);
+                            st(di, i * p.dinitial_states_stride[2], acc);
+                        }
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // a chunk is clean when its window [cs-H, cs+NS+H) lies inside the
+        // sequence (the last H positions: dfinal_states reach back that far)
+        // and, with seq_idx, carries one id >= 0
+        auto steps = [&](const Chunk& ch, int32_t cs, auto ns, auto accc, auto headc) {
+            constexpr int NS = decltype(ns)::value;
+            bool clean = cs >= H && cs + NS + H <= L;
+            if constexpr (SEQ) {
+                const int32_t id0 = ch.ids[0];
+                bool same = id0 >= 0;
+#pragma unroll
+                for (int i = 1; i < NS + H; ++i) same = same && ch.ids[i] == id0;
+                clean = clean && same;
+            }
+            if (clean) steps_clean(ch, cs, ns, accc, headc);
+            else steps_gated(ch, cs, ns, accc);
+        };
+
+        constexpr std::integral_constant<int, G> kG{};
+        constexpr std::integral_constant<int, H> kH{};
+        constexpr std::true_type kAcc{};
+        constexpr std::false_type kNoAcc{};
+        constexpr std::true_type kHead{};
+        constexpr std::false_type kBody{};
+        if constexpr (NCH == 1) {
+            // the whole run at once: its rows and the tail's are all in flight
+            load(t0 + R, B, kH);  // the tail: the next run's first H rows
+            steps(A, t0, kG, kAcc, kHead);
+            steps(B, t0 + R, kH, kNoAcc, kBody);
+        } else {
+            // chunk 0 in A, chunk 1 in B; then chunks in pairs, each buffer
+            // refilled as soon as it has been consumed; the tail last
+            load(t0 + G, B, kG);
+            steps(A, t0, kG, kAcc, kHead);
+#pragma unroll 1
+            for (int c = 1; c + 1 < NCH; c += 2) {
+                const int32_t cb = t0 + c * G;
+                load(cb + G, A, kG);
+                steps(B, cb, kG, kAcc, kBody);
+                load(cb + 2 * G, B, kG);
+                steps(A, cb + G, kG, kAcc, kBody);
+            }
+            load(t0 + R, A, kH);  // the tail: the next run's first H rows
+            steps(B, t0 + R - G, kG, kAcc, kBody);
+            steps(A, t0 + R, kH, kNoAcc, kBody);
+        }
         if (!active) {
 #pragma unroll
             for (int e = 0; e < CPL; ++e) {
-                part.pb[e] = 0.0f;
+                s.pb[e] = 0.0f;
 #pragma unroll
-                for (int k = 0; k < W; ++k) part.pw[k][e] = 0.0f;
+                for (int k = 0; k < W; ++k) s.pw[k][e] = 0.0f;
             }
         }
     }
 
-    // ---- weight / bias gradient: sum the block's tiles in LDS, then
-    //      consecutive fp32 atomics ----
+    // ---- weight / bias gradient: sum the block's runs in LDS, then
+    //      consecutive fp32 atomics (or the block's record) ----
     float* rr = red[wave];
 #pragma unroll
     for (int e = 0; e < CPL; ++e) {
 #pragma unroll
-        for (int k = 0; k < W; ++k) rr[(lane * CPL + e) * W + k] = part.pw[k][e];
-        rr[NC * W + lane * CPL + e] = part.pb[e];
+        for (int k = 0; k < W; ++k) rr[(lane * CPL + e) * W + k] = s.pw[k][e];
+        rr[NC * W + lane * CPL + e] = s.pb[e];
     }
     __syncthreads();
     constexpr int NE = NC * (W + 1);
@@ -950,12 +986,12 @@ bool cl_ok(const cc1d_bwd_params& p) {
     if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.dout_stride[0] % CPL || p.dout_stride[2] % CPL ||
         p.dx_stride[0] % CPL || p.dx_stride[2] % CPL)
         return false;
-    const int64_t span = p.seqlen + kClTS + 16;  // furthest row a tile touches
+    const int64_t span = p.seqlen + kClWPB * kClR + 16;  // past the furthest run start
     const int64_t lim = (int64_t)1 << 31;
     if (p.dim >= lim || span * p.x_stride[2] >= lim || span * p.dout_stride[2] >= lim || span * p.dx_stride[2] >= lim)
         return false;
     if (p.seq_idx != nullptr && span * p.seq_idx_stride[1] >= lim) return false;
-    if (p.batch * ceil_div(p.dim / CPL, 64) * ceil_div(ceil_div(p.seqlen, kClTS), kClWPB) >= lim) return false;
+    if (p.batch * ceil_div(p.dim / CPL, 64) * ceil_div(p.seqlen, kClR * kClWPB) >= lim) return false;
     return true;
 }
 
@@ -1003,8 +1039,8 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         pl.kind = kBwdCl;
         pl.cpl = CPL;
         pl.a.groups = ceil_div(p.dim / CPL, 64);
-        pl.a.chunk = kClTS;
-        pl.a.nseg = ceil_div(ceil_div(p.seqlen, kClTS), kClWPB);  // tile groups per row
+        pl.a.chunk = kClR;
+        pl.a.nseg = ceil_div(p.seqlen, kClR * kClWPB);  // run groups per row
         pl.a.n_items = 0;
         pl.blocks = p.batch * pl.a.groups * pl.a.nseg;
         pl.records = pl.blocks;
@@ -1037,10 +1073,10 @@ int launch_plan(BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream) {
         return CC1D_ERR_SHAPE;  // not reached: the plan only picks rows when the halo fits
     }
     if (pl.kind == kBwdCl) {
-        constexpr int CPL = 4 / (int)sizeof(T);
         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
             constexpr bool SEQ = decltype(qc)::value;
-            bwd_cl<T, W, CPL, kClTS, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
+            constexpr int G = W - 1 <= kClG ? kClG : 2 * kClG;  // at least H steps per chunk
+            bwd_clw<T, W, G, kClR, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
             return launch_status();
         });
     }

@@ -291,5 +291,13 @@ __device__ __forceinline__ int64_t uniform(int64_t v) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
+// A per-lane value the compiler can neither see through nor move: address
+// arithmetic of a rarely taken branch that uses it stays inside the branch
+// instead of being hoisted out of the loop around it (where it would hold
+// registers for the whole loop).
+__device__ __forceinline__ int32_t opaque(int32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
 
 }  // namespace cc1d

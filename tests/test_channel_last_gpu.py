@@ -159,9 +159,36 @@ def test_cl_backward_states(dtype, width, seqlen):
 
 
 def test_cl_backward_many_tile_groups():
-    """Several blocks of tiles per row and several batches: the LDS block reduction feeds each
-    channel's accumulators from many blocks."""
-    x, w, b, _ = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16)
-    dout = make_inputs(3, 256, 1000, 4, dtype=torch.bfloat16, seed=1)[0]
+    """Several blocks per row (1024 time steps each) and several batches: the LDS block
+    reduction feeds each channel's accumulators from many blocks, and every run hands its
+    last dx rows across a chunk, run and block edge (the sequence ends inside a run)."""
+    x, w, b, _ = make_inputs(3, 256, 2600, 4, dtype=torch.bfloat16)
+    dout = make_inputs(3, 256, 2600, 4, dtype=torch.bfloat16, seed=1)[0]
     _check(_grads(x, w, b, dout), O.causal_conv1d_bwd(x, w, b, dout, activation="silu"), torch.bfloat16,
            scales(x, w, b, dout, activation="silu"))
+
+
+# sequence starts on and next to the edges of 4- and 8-step chunks, 128-step runs and
+# 1024-step blocks, a padding stretch (-1) across a run edge, and an id that comes back
+_EDGE_CUTS = [1, 3, 4, 127, 128, 131, 700, 1021, 1024, 1025, 1600, 2047, 2048, 2300]
+
+
+def _edge_seq_idx(batch, seqlen):
+    ids = torch.zeros(batch, seqlen, dtype=torch.int32)
+    for i, c in enumerate(_EDGE_CUTS):
+        ids[:, c:] = i + 1
+    ids[:, 1900:2010] = -1
+    ids[:, 2400:2450] = 5
+    ids[1] = ids[1].roll(37)
+    return ids
+
+
+@pytest.mark.parametrize("dtype,width", [(torch.bfloat16, 4), (torch.float32, 3), (torch.float16, 7),
+                                         (torch.bfloat16, 9)])
+def test_cl_backward_seq_idx_run_edges(dtype, width):
+    """seq_idx boundaries at chunk, run and block edges over several blocks per row."""
+    x, w, b, _ = make_inputs(2, 256, 2600, width, dtype=dtype)
+    dout = make_inputs(2, 256, 2600, width, dtype=dtype, seed=1)[0]
+    s = _edge_seq_idx(2, 2600)
+    _check(_grads(x, w, b, dout, seq_idx=s), O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation="silu"))
