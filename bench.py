@@ -174,7 +174,8 @@ class Floors:
         lib.cc1d_floor_copy.argtypes = [vp, vp, i64, vp]
         lib.cc1d_floor_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
         lib.cc1d_floor_chunks.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, vp]
-        for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks):
+        lib.cc1d_floor_tiles.argtypes = [vp, vp, vp, i64, i64, i32, vp]
+        for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks, lib.cc1d_floor_tiles):
             f.restype = i32
         self.lib = lib
 
@@ -193,6 +194,12 @@ class Floors:
                                              x.shape[0], xvec, pool[0].numel() * pool.element_size() // 16,
                                              pool.shape[0], ratio, torch.cuda.current_stream().cuda_stream),
                     "cc1d_floor_rows")
+
+    def tiles(self, torch, x, g, out, seg):
+        """x, g, out: (rows, row) tensors, contiguous rows"""
+        self._check(self.lib.cc1d_floor_tiles(x.data_ptr(), g.data_ptr(), out.data_ptr(), x.shape[0],
+                                              x.shape[1] * x.element_size(), seg,
+                                              torch.cuda.current_stream().cuda_stream), "cc1d_floor_tiles")
 
     def chunks(self, torch, x, out, pool, idx, cs, nchunks):
         line_chunks = pool.shape[2] * pool.element_size() // 16
@@ -345,7 +352,7 @@ def _c4a_cases(torch, cc, floors):
     return cases
 
 
-def _c3_cases(torch):
+def _c3_cases(torch, floors=None):
     ops = torch.ops.causal_conv1d_amd
     cases = {}
     # C3: stored (1, 8192, 4096) bf16 channel-last, viewed (1, 4096, 8192); W4, SiLU, no bias
@@ -385,7 +392,16 @@ def _c3_cases(torch):
         fns = [lambda x=x, d=d, dx=dx, sb=sb, ib=ib, dib=dib: ops._bwd_typed_inplace(
             x, w3, None, d, sb, ib, None, dx, dw3t, None, dib, True) for x, d, _, dx in sets]
         cases[f"{name}_bwd_typed"] = (fns, 3 * n3 + extra_t, 1,
-                                      {"op": "_bwd_typed_inplace (the autograd backward: bwd_cl + bwd_reduce)"})
+                                      {"op": "_bwd_typed_inplace (the autograd backward: bwd_clw + bwd_reduce)"})
+    if floors is not None:
+        # the backward's access pattern with no arithmetic: x and dout read, dx written, on
+        # the same sets (rows of 8 KB); seg 256: a wavefront per 16 rows x 256 bytes (a dword
+        # per lane, the kernel's own slices); seg 1024: 4 rows x 1 KB (16 bytes per lane)
+        for seg in (256, 1024):
+            fns = [lambda x=x, d=d, dx=dx, seg=seg: floors.tiles(
+                torch, x.transpose(1, 2)[0], d.transpose(1, 2)[0], dx.transpose(1, 2)[0], seg)
+                for x, d, _, dx in sets]
+            cases[f"floor_tiles{seg}_c3"] = (fns, 3 * n3, 1, {})
     return cases, (cuts, L3, D3)
 
 
@@ -452,8 +468,12 @@ def _run_cases(torch, cases, launches, runs, res):
 def bench_configs(torch, cc, floors, args):
     """Every kernel at the other benchmark configurations (reported, not the headline)."""
     res = {}
-    c3, c3info = _c3_cases(torch)
+    c3, c3info = _c3_cases(torch, floors)
     _run_cases(torch, c3, args.launches, args.runs, res)
+    for name in ("c3a_bwd", "c3b_bwd", "c3a_bwd_typed", "c3b_bwd_typed"):
+        if "floor_tiles256_c3" in res:
+            res[name]["floor_same_pattern_us"] = res["floor_tiles256_c3"]["us_per_launch"]
+            res[name]["floor_widest_pattern_us"] = res["floor_tiles1024_c3"]["us_per_launch"]
     del c3
     torch.cuda.empty_cache()
     c5 = _c5_cases(torch)
@@ -570,7 +590,7 @@ def mode_kernels(torch, cc, floors, args):
     cases = dict(_c2_cases(torch, sets, w, b))
     cases.update(_c4a_cases(torch, cc, floors))
     if not args.no_configs:
-        c3, c3info = _c3_cases(torch)
+        c3, c3info = _c3_cases(torch, floors)
         cases.update(c3)
         cases.update(_c5_cases(torch))
         cases.update(_c4b_cases(torch, cc, floors)[0])

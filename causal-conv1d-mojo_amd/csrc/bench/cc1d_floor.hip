@@ -15,6 +15,12 @@
 //                        back in place; one wavefront per 64 x vectors and
 //                        the 64 * R state vectors of the same channels, all
 //                        accesses coalesced.
+//   cc1d_floor_tiles  -- the channel-last backward's pattern: two tensors of
+//                        rows (time steps) of row_bytes are read and a third
+//                        written (out = x ^ g ^ 1), a wavefront taking
+//                        `rows` consecutive rows of a seg-byte column slice
+//                        (seg 256: a dword per lane, the kernel's own shape;
+//                        seg 1024: 16 bytes per lane, the widest row pieces).
 //   cc1d_floor_chunks -- the circular decode update's pattern: per (b, c),
 //                        read and write back `chunks` consecutive 16-byte
 //                        chunks of state line (idx[b], c) starting at chunk
@@ -22,6 +28,8 @@
 //                        out `xwords` dwords.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -90,6 +98,27 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
     for (int j = 0; j < chunks; ++j) line[(k + j) % line_chunks] = flip(v[j]);
 }
 
+// grid: (slices per row) x (row tiles / 4), 4 wavefronts per block on
+// consecutive row tiles of one slice; all loads first, then all stores
+template <int NB, int ROWS>
+__global__ void __launch_bounds__(256) floor_tiles(const char* __restrict__ x, const char* __restrict__ g,
+                                                   char* __restrict__ out, int64_t row_bytes, int nslice) {
+    typedef typename std::conditional<NB == 16, u32x4, uint32_t>::type V;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int slice = blockIdx.x % nslice;
+    const int64_t tile = (int64_t)(blockIdx.x / nslice) * 4 + wave;
+    const int64_t base = tile * ROWS * row_bytes + (int64_t)slice * 64 * NB + lane * NB;
+    V xv[ROWS], gv[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        xv[r] = *reinterpret_cast<const V*>(x + base + r * row_bytes);
+        gv[r] = *reinterpret_cast<const V*>(g + base + r * row_bytes);
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+        __builtin_nontemporal_store(xv[r] ^ gv[r] ^ (V)1u, reinterpret_cast<V*>(out + base + r * row_bytes));
+}
+
 bool launched() { return hipGetLastError() == hipSuccess; }
 
 }  // namespace
@@ -126,6 +155,28 @@ int cc1d_floor_rows(const void* x, void* out, void* pool, const int32_t* idx, in
     case 3: floor_rows<3><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
     default: floor_rows<4><<<grid, 64, 0, s>>>(xv, ov, pv, idx, (uint32_t)xvec, (uint32_t)pool_row_vec, (int32_t)pool_rows); break;
     }
+    return launched() ? 0 : -2;
+}
+
+// x, g, out: `rows` rows of row_bytes each (16-byte aligned); seg 256
+// (16 rows per wavefront) or 1024 (4 rows per wavefront); row_bytes a
+// multiple of seg and rows a multiple of 4 * rows per wavefront
+int cc1d_floor_tiles(const void* x, const void* g, void* out, int64_t rows, int64_t row_bytes, int seg,
+                     void* stream) {
+    const int per = seg == 256 ? 16 : 4;
+    if ((seg != 256 && seg != 1024) || rows < 0 || row_bytes <= 0 || row_bytes % seg || rows % (4 * per))
+        return -1;
+    if (rows == 0) return 0;
+    if (x == nullptr || g == nullptr || out == nullptr) return -1;
+    const int nslice = (int)(row_bytes / seg);
+    const int64_t blocks = nslice * (rows / (4 * per));
+    if (blocks >= ((int64_t)1 << 31)) return -1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const char* xc = static_cast<const char*>(x);
+    const char* gc = static_cast<const char*>(g);
+    char* oc = static_cast<char*>(out);
+    if (seg == 256) floor_tiles<4, 16><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
+    else floor_tiles<16, 4><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
     return launched() ? 0 : -2;
 }
 

@@ -72,3 +72,17 @@ def test_chunks_floor(floors, nchunks):
             k = (c % line_chunks + j) % line_chunks
             want[r, :, k] = _flip(want[r, :, k])
     assert torch.equal(pool, want.view(P, D, S))
+
+
+@pytest.mark.parametrize("seg", [256, 1024])
+def test_tiles_floor(floors, seg):
+    rows, width = 128, 1024  # bf16 rows of 2 KB
+    g = torch.Generator(device=DEV).manual_seed(2)
+    x = torch.randn(rows + 3, width, generator=g, device=DEV).bfloat16()
+    d = torch.randn(rows + 3, width, generator=g, device=DEV).bfloat16()
+    out = torch.zeros_like(x)
+    floors.tiles(torch, x[:rows], d[:rows], out[:rows], seg)
+    torch.cuda.synchronize()
+    want = x[:rows].view(torch.int32) ^ d[:rows].view(torch.int32) ^ 1  # bit patterns (some are NaNs)
+    assert torch.equal(out[:rows].view(torch.int32), want)
+    assert torch.all(out[rows:].view(torch.int16) == 0)
