@@ -310,6 +310,17 @@ def _c2_cases(torch, sets, w, b):
     }
 
 
+def _c2_floor_cases(torch, sets, floors):
+    """The C2 backward's streams with no arithmetic: x and dout read, dx written, on the
+    same sets viewed as (B * D) rows of 4 KB: a wavefront per 4 rows x 1 KB, or per row
+    (4 KB, the backward kernel's own item), 16 bytes per lane per load."""
+    bufs = [(x.detach().reshape(B * D, L), dout.reshape(B * D, L), torch.empty(B * D, L, dtype=x.dtype,
+                                                                                 device=x.device))
+            for x, dout in sets]
+    return {f"floor_tiles{seg}_c2": ([lambda u=u, seg=seg: floors.tiles(torch, u[0], u[1], u[2], seg) for u in bufs],
+                                     3 * B * D * L * 2, 1, {}) for seg in (1024, 4096)}
+
+
 def _update_sets(torch, n, seqlen=1, S=W - 1, seed=7):
     sets = []
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -588,6 +599,7 @@ def mode_kernels(torch, cc, floors, args):
     """Eager launch loop (for rocprofv3 kernel traces / counters)."""
     sets, w, b = _c2_sets(torch, 4)
     cases = dict(_c2_cases(torch, sets, w, b))
+    cases.update(_c2_floor_cases(torch, sets, floors))
     cases.update(_c4a_cases(torch, cc, floors))
     if not args.no_configs:
         c3, c3info = _c3_cases(torch, floors)
@@ -638,8 +650,12 @@ def main():
     ms = bench_step(torch, cc, args, sets, w, b)
     kern = {}
     _run_cases(torch, _c2_cases(torch, sets, w, b), args.launches, args.runs, kern)
+    _run_cases(torch, _c2_floor_cases(torch, sets, floors), args.launches, args.runs, kern)
     for k in ("fwd", "bwd", "bwd_typed"):
         kern[k]["buffer_sets"] = nsets
+    for k in ("bwd", "bwd_typed"):
+        kern[k]["floor_same_streams_us"] = kern["floor_tiles4096_c2"]["us_per_launch"]
+        kern[k]["floor_streams_4rows_us"] = kern["floor_tiles1024_c2"]["us_per_launch"]
     del sets
     torch.cuda.empty_cache()
     _run_cases(torch, _c4a_cases(torch, cc, floors), args.launches, args.runs, kern)
@@ -688,6 +704,7 @@ def main():
             "us_per_launch": bwd["us_per_launch"],
             "us_min": bwd["us_min"],
             "us_max": bwd["us_max"],
+            "floor_same_streams_us": bwd["floor_same_streams_us"],
         },
         "kernels": kern,
         "cpu_baseline": cpu,

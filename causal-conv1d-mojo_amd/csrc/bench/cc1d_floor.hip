@@ -19,8 +19,10 @@
 //                        rows (time steps) of row_bytes are read and a third
 //                        written (out = x ^ g ^ 1), a wavefront taking
 //                        `rows` consecutive rows of a seg-byte column slice
-//                        (seg 256: a dword per lane, the kernel's own shape;
-//                        seg 1024: 16 bytes per lane, the widest row pieces).
+//                        (seg 256: a dword per lane, 16 rows, the channel-
+//                        last kernel's shape; seg 1024: 16 bytes per lane, 4
+//                        rows; seg 4096: 4 x 16 bytes per lane, one row, the
+//                        channel-first kernel's shape).
 //   cc1d_floor_chunks -- the circular decode update's pattern: per (b, c),
 //                        read and write back `chunks` consecutive 16-byte
 //                        chunks of state line (idx[b], c) starting at chunk
@@ -99,24 +101,31 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
 }
 
 // grid: (slices per row) x (row tiles / 4), 4 wavefronts per block on
-// consecutive row tiles of one slice; all loads first, then all stores
-template <int NB, int ROWS>
+// consecutive row tiles of one slice; a lane moves VPL vectors of NB bytes
+// per row (vector v at byte (v * 64 + lane) * NB of the slice); all loads
+// first, then all stores
+template <int NB, int VPL, int ROWS>
 __global__ void __launch_bounds__(256) floor_tiles(const char* __restrict__ x, const char* __restrict__ g,
                                                    char* __restrict__ out, int64_t row_bytes, int nslice) {
     typedef typename std::conditional<NB == 16, u32x4, uint32_t>::type V;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int slice = blockIdx.x % nslice;
     const int64_t tile = (int64_t)(blockIdx.x / nslice) * 4 + wave;
-    const int64_t base = tile * ROWS * row_bytes + (int64_t)slice * 64 * NB + lane * NB;
-    V xv[ROWS], gv[ROWS];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        xv[r] = *reinterpret_cast<const V*>(x + base + r * row_bytes);
-        gv[r] = *reinterpret_cast<const V*>(g + base + r * row_bytes);
-    }
+    const int64_t base = tile * ROWS * row_bytes + (int64_t)slice * 64 * NB * VPL + lane * NB;
+    V xv[ROWS][VPL], gv[ROWS][VPL];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r)
-        __builtin_nontemporal_store(xv[r] ^ gv[r] ^ (V)1u, reinterpret_cast<V*>(out + base + r * row_bytes));
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+            xv[r][v] = *reinterpret_cast<const V*>(x + base + r * row_bytes + v * 64 * NB);
+            gv[r][v] = *reinterpret_cast<const V*>(g + base + r * row_bytes + v * 64 * NB);
+        }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            __builtin_nontemporal_store(xv[r][v] ^ gv[r][v] ^ (V)1u,
+                                        reinterpret_cast<V*>(out + base + r * row_bytes + v * 64 * NB));
 }
 
 bool launched() { return hipGetLastError() == hipSuccess; }
@@ -159,12 +168,13 @@ int cc1d_floor_rows(const void* x, void* out, void* pool, const int32_t* idx, in
 }
 
 // x, g, out: `rows` rows of row_bytes each (16-byte aligned); seg 256
-// (16 rows per wavefront) or 1024 (4 rows per wavefront); row_bytes a
+// (16 rows per wavefront), 1024 (4 rows) or 4096 (1 row); row_bytes a
 // multiple of seg and rows a multiple of 4 * rows per wavefront
 int cc1d_floor_tiles(const void* x, const void* g, void* out, int64_t rows, int64_t row_bytes, int seg,
                      void* stream) {
-    const int per = seg == 256 ? 16 : 4;
-    if ((seg != 256 && seg != 1024) || rows < 0 || row_bytes <= 0 || row_bytes % seg || rows % (4 * per))
+    const int per = seg == 256 ? 16 : (seg == 1024 ? 4 : 1);
+    if ((seg != 256 && seg != 1024 && seg != 4096) || rows < 0 || row_bytes <= 0 || row_bytes % seg ||
+        rows % (4 * per))
         return -1;
     if (rows == 0) return 0;
     if (x == nullptr || g == nullptr || out == nullptr) return -1;
@@ -175,8 +185,9 @@ int cc1d_floor_tiles(const void* x, const void* g, void* out, int64_t rows, int6
     const char* xc = static_cast<const char*>(x);
     const char* gc = static_cast<const char*>(g);
     char* oc = static_cast<char*>(out);
-    if (seg == 256) floor_tiles<4, 16><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
-    else floor_tiles<16, 4><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
+    if (seg == 256) floor_tiles<4, 1, 16><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
+    else if (seg == 1024) floor_tiles<16, 1, 4><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
+    else floor_tiles<16, 4, 1><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
     return launched() ? 0 : -2;
 }
 

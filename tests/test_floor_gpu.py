@@ -74,9 +74,9 @@ def test_chunks_floor(floors, nchunks):
     assert torch.equal(pool, want.view(P, D, S))
 
 
-@pytest.mark.parametrize("seg", [256, 1024])
+@pytest.mark.parametrize("seg", [256, 1024, 4096])
 def test_tiles_floor(floors, seg):
-    rows, width = 128, 1024  # bf16 rows of 2 KB
+    rows, width = 128, 2048  # bf16 rows of 4 KB
     g = torch.Generator(device=DEV).manual_seed(2)
     x = torch.randn(rows + 3, width, generator=g, device=DEV).bfloat16()
     d = torch.randn(rows + 3, width, generator=g, device=DEV).bfloat16()
