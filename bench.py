@@ -444,7 +444,7 @@ def _c4b_cases(torch, cc, floors):
     nsets = -(-2 * MALL_BYTES // C4B_LINE_BYTES) + 1  # 5: whole lines touched between reuses > 2x MALL
     sets, w, b = _update_sets(torch, nsets, seqlen=4, S=C4B_S, seed=11)
     fns = [lambda u=u: cc._native.native_update(u[0], w, b, u[1], u[2], u[3], u[4], True) for u in sets]
-    hbm = _pmc("update_c4b")
+    hbm = _pmc("c4b_update")
     extra = {"buffer_sets": nsets, "note": "14 of 128 bytes of each state line are touched; DRAM bursts bound this"}
     cases = {"update_c4b": (fns, C4B_BYTES, 1, extra)}
     if floors is not None:

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import sys
 from pathlib import Path
 
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
@@ -95,6 +96,8 @@ _lib = None
 
 
 def library_path() -> Path:
+    """The in-tree library; CC1D_AMD_LIB may name another build of it (announced on
+    stderr when the library is loaded, so a stray variable cannot go unnoticed)."""
     return Path(os.environ.get("CC1D_AMD_LIB", _LIB_PATH))
 
 
@@ -109,6 +112,9 @@ def load():
             f"causal_conv1d_amd: native library {path} is not built; "
             "run `python causal-conv1d-mojo_amd/csrc/build.py`"
         )
+    if path.resolve() != _LIB_PATH.resolve():
+        print(f"causal_conv1d_amd: loading {path} (CC1D_AMD_LIB), not the in-tree {_LIB_PATH}",
+              file=sys.stderr, flush=True)
     lib = ctypes.CDLL(str(path))
     lib.cc1d_abi_version.restype = ctypes.c_int
     lib.cc1d_abi_version.argtypes = []
