@@ -11,7 +11,12 @@
 //   out-of-pool index zeroes out[b] and leaves the pool untouched.
 //
 // Kernels
-//   update_lin     -- linear mode, one token, S == W-1, channel-contiguous x /
+//   update_dir     -- linear mode, one token, S == W-1 <= 4, channel-contiguous
+//                     x / out and contiguous state rows: a lane owns one dword
+//                     of x (2 bf16/fp16 channels, 1 fp32) of two batch
+//                     entries and loads the channels' state span (H dwords)
+//                     directly, one load per span; no LDS.
+//   update_lin     -- the same for W > 5: one token, S == W-1, channel-contiguous x /
 //                     out and contiguous state rows: one wavefront per (batch
 //                     entry, 16 * EPV channels) moves the group's state and x
 //                     spans as consecutive 16-byte vectors, one per lane at
@@ -119,7 +124,7 @@ template <typename T> struct LinArgs {
     uint32_t x_row, out_row, state_row;  // row strides (elements) of x, out, the state pool
     uint32_t dim;
     int32_t state_rows;
-    int32_t unused;
+    uint32_t nbatch;  // batch entries (update_dir)
 };
 
 // Linear mode, seqlen 1, state_len == W-1 (H), channel-contiguous x / out and
@@ -267,6 +272,137 @@ __global__ void __launch_bounds__(64) update_lin(const LinArgs<T> a) {
             if (row >= 0 && vi < nsv) vstore(sp + vi * EPV, r);
         } else if (vi - NSV < nxv) {
             vstore(orow + (vi - NSV) * EPV, r);
+        }
+    }
+}
+
+// Linear mode, seqlen 1, state_len == W-1 (H <= 4): a lane owns NS dwords of
+// x (CPL channels each: 2 bf16/fp16, 1 fp32; dwords lane, lane + 64, ...) and
+// reads their H-dword state spans directly, one dword-vector load per span;
+// consecutive lanes hold consecutive spans, so each load instruction covers
+// 64 * 4H contiguous bytes. No LDS and no shuffle between the loads, the
+// arithmetic and the stores. A wavefront takes 64 * NS * CPL channels of BPW
+// batch entries (grid: channel groups x batch-entry groups); x first, then
+// the BPW pool indices (scalar loads) behind a scheduling fence, then the
+// state spans, then the weights and bias (cache-resident), all before any
+// arithmetic.
+template <typename T, int W, int BPW, int NS, bool SILU, bool HAS_BIAS, bool HAS_IDX>
+__global__ void __launch_bounds__(64) update_dir(const LinArgs<T> a) {
+    constexpr int H = W - 1;
+    constexpr int CPL = 4 / (int)sizeof(T);
+    static_assert(H >= 1 && H <= 4, "one dword vector of state per span");
+    const int lane = threadIdx.x;
+    uint32_t c[NS];
+    bool on[NS];
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        const uint32_t cu = (blockIdx.x * (64 * NS) + 64 * u + lane) * CPL;
+        on[u] = cu < a.dim;
+        c[u] = on[u] ? cu : 0;  // lanes past the end read channel 0 and store nothing
+    }
+    const uint32_t b0 = blockIdx.y * BPW;
+    const uint32_t nb = a.nbatch;
+    // the first entry's index address, formed (in scalar registers) before the x loads
+    const int32_t* ip = HAS_IDX ? a.idx + b0 : nullptr;
+    if constexpr (HAS_IDX) asm volatile("" ::"s"(ip));
+    uint32_t xd[BPW][NS];
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+        const uint32_t b = min(b0 + q, nb - 1);
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+            xd[q][u] = *reinterpret_cast<const uint32_t*>(a.x + (size_t)b * a.x_row + c[u]);
+    }
+    // the pool indices (scalar loads) after the index-free x loads; the fence
+    // keeps the compiler from hoisting them and their wait above those
+    __builtin_amdgcn_sched_barrier(0);
+    int32_t row[BPW];
+    if constexpr (HAS_IDX) {
+        int32_t r[BPW];
+        // one scalar load for a pair when both entries exist and the pair is 8-byte aligned
+        if (BPW == 2 && b0 + 1 < nb && (reinterpret_cast<uintptr_t>(ip) & 7u) == 0) {
+            const uint64_t two = *(const __attribute__((address_space(4))) uint64_t*)reinterpret_cast<uintptr_t>(ip);
+            r[0] = (int32_t)(uint32_t)two;
+            r[BPW - 1] = (int32_t)(uint32_t)(two >> 32);
+        } else {
+#pragma unroll
+            for (int q = 0; q < BPW; ++q) r[q] = ld_uniform(ip + (b0 + q < nb ? q : 0));
+        }
+#pragma unroll
+        for (int q = 0; q < BPW; ++q)
+            row[q] = (r[q] < 0 || r[q] >= a.state_rows) ? -1 : r[q];  // padding (any negative) or out of the pool
+    } else {
+#pragma unroll
+        for (int q = 0; q < BPW; ++q) row[q] = (int32_t)(b0 + q);
+    }
+    uint32_t st[BPW][NS][H];
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+        const T* srow = a.conv_state + (size_t)(row[q] >= 0 ? row[q] : 0) * a.state_row;
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const uint32_t* sp = reinterpret_cast<const uint32_t*>(srow + (size_t)c[u] * H);
+#pragma unroll
+            for (int i = 0; i < H; ++i) st[q][u][i] = sp[i];
+        }
+    }
+    // weights and bias (cache-resident) after the state loads: they arrive
+    // with the state instead of holding the state loads' issue back
+    uint32_t wd[NS][W], bd[NS];  // CPL * W weights and CPL biases per span, raw
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(a.weight + (size_t)c[u] * W);
+#pragma unroll
+        for (int k = 0; k < W; ++k) wd[u][k] = wp[k];
+        bd[u] = HAS_BIAS ? *reinterpret_cast<const uint32_t*>(a.bias + c[u]) : 0u;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load is issued before any arithmetic
+    auto elem = [&](const uint32_t* d, int n) -> uint32_t {
+        if constexpr (CPL == 1) return d[n];
+        else return (n & 1) ? (d[n >> 1] >> 16) : (d[n >> 1] & 0xffffu);
+    };
+    auto as_f32 = [&](uint32_t bits) -> float {
+        if constexpr (CPL == 1) return __uint_as_float(bits);
+        else return to_f32(T{(uint16_t)bits});
+    };
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            uint32_t sraw[CPL * H], nraw[CPL * H];
+#pragma unroll
+            for (int n = 0; n < CPL * H; ++n) sraw[n] = elem(st[q][u], n);
+            float o[CPL];
+#pragma unroll
+            for (int e = 0; e < CPL; ++e) {
+                const uint32_t xb = elem(&xd[q][u], e);
+                float win[W], w[W];
+#pragma unroll
+                for (int i = 0; i < H; ++i) win[i] = as_f32(sraw[e * H + i]);
+                win[H] = as_f32(xb);
+#pragma unroll
+                for (int k = 0; k < W; ++k) w[k] = as_f32(elem(wd[u], e * W + k));
+                const float bias = HAS_BIAS ? as_f32(elem(&bd[u], e)) : 0.0f;
+                float acc = conv_taps<W>(bias, w, win);
+                if constexpr (SILU) acc = silu(acc);
+                o[e] = acc;
+#pragma unroll
+                for (int i = 0; i < H; ++i) nraw[e * H + i] = i + 1 < H ? sraw[e * H + i + 1] : xb;
+            }
+            uint32_t od;
+            if constexpr (CPL == 1) od = __float_as_uint(o[0]);
+            else od = pack2<T>(o[0], o[1]);
+            if (row[q] < 0) od = 0u;  // padding entry: zero output, state untouched
+            if (on[u] && b0 + q < nb) {  // (an entry past the batch computed on clamped data)
+                *reinterpret_cast<uint32_t*>(a.out + (size_t)(b0 + q) * a.out_row + c[u]) = od;
+                if (row[q] >= 0) {
+                    uint32_t* sp = reinterpret_cast<uint32_t*>(a.conv_state + (size_t)row[q] * a.state_row +
+                                                               (size_t)c[u] * H);
+#pragma unroll
+                    for (int i = 0; i < H; ++i)
+                        sp[i] = CPL == 1 ? nraw[i] : (nraw[2 * i] | (nraw[2 * i + 1] << 16));
+                }
+            }
         }
     }
 }
@@ -504,6 +640,14 @@ namespace {
 // update_lin: 16-byte vectors per lane (each wavefront covers 16 * EPV * kLinNV
 // channels). C4a (256 x 5120 bf16, W4): 1 -> 7.58 us, 2 -> 7.12 us, 4 -> 7.50 us.
 constexpr int kLinNV = 2;
+// update_dir: batch entries per wavefront and dwords of x per lane. C4a (A/B
+// on one box, update_lin 7.14 us): 2 x 1 -> 6.97 us; 1 x 1 7.06; 4 x 1 7.03;
+// 2 x 2 7.38; 1 x 2 7.15; 1 x 4 7.48; 4 x 2 7.80. Without SiLU, or with the
+// weights and bias replaced by constants, 2 x 1 measures the same 6.97-7.05 us:
+// what is left is the access pattern (a copy that moves the same bytes as
+// 16-byte vectors, one x and three state vectors per lane, takes ~0.4 us less).
+constexpr int kDirBPW = 2;
+constexpr int kDirNS = 1;
 
 template <typename T>
 bool lin_ok(const cc1d_update_params& p) {
@@ -576,7 +720,18 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                     la.state_row = (uint32_t)p.conv_state_stride[0];
                     la.dim = (uint32_t)p.dim;
                     la.state_rows = (int32_t)p.state_rows;
-                    la.unused = 0;
+                    la.nbatch = (uint32_t)p.batch;
+                    if constexpr (W - 1 <= 4) {
+                        constexpr int CPL = 4 / (int)sizeof(T);
+                        const dim3 gd((unsigned)ceil_div(p.dim, 64 * kDirNS * CPL), (unsigned)ceil_div(p.batch, kDirBPW));
+                        return with_flag(p.bias != nullptr, [&](auto hb) {
+                            return with_flag(p.conv_state_indices != nullptr, [&](auto hi) {
+                                update_dir<T, W, kDirBPW, kDirNS, SILU, decltype(hb)::value, decltype(hi)::value>
+                                    <<<gd, 64, 0, stream>>>(la);
+                                return launch_status();
+                            });
+                        });
+                    }
                     // grid: channel groups x batch entries (no division in the kernel)
                     const dim3 grid((unsigned)ceil_div(p.dim, 16 * EPV * kLinNV), (unsigned)p.batch);
                     return with_flag(p.bias != nullptr, [&](auto hb) {

@@ -193,6 +193,34 @@ def test_padding_and_out_of_pool_rows(dtype, dim, circular):
     assert_equal(sg2.cpu(), st)
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 3, 4, 5])
+@pytest.mark.parametrize("dim", [130, 200])  # a partial last channel group
+def test_odd_batch_offset_indices(dtype, width, dim):
+    """Two batch entries per wavefront with an odd batch (the last wavefront's second entry is
+    past the end), indices read from a view at a 4-byte (not 8-byte) aligned address, and a
+    channel group that ends inside a wavefront."""
+    B, P = 7, 9
+    full = torch.tensor([99, 3, 0, -1, 8, 5, -3, 1], dtype=torch.int32)
+    idx = full.to(DEV)[1:]  # storage offset of one int32
+    assert idx.data_ptr() % 8 == 4
+    x, w, b, _ = make_inputs(B, dim, 1, width, dtype=dtype)
+    pool = make_inputs(P, dim, width - 1, width, dtype=dtype, seed=1)[0]
+    sg = pool.to(DEV)
+    og = torch.full((B, dim, 1), float("nan"), dtype=dtype, device=DEV)
+    native_update(x.to(DEV), w.to(DEV), b.to(DEV), sg, idx, None, og, True)
+    out, st = og[..., 0].cpu(), sg.cpu()
+    ids = full[1:]
+    real = (ids >= 0).nonzero().flatten()
+    assert torch.all(out[(ids < 0).nonzero().flatten()] == 0)
+    rs = pool[ids[real].long()].clone()
+    rout = O.causal_conv1d_update(x[real, :, 0], rs, w, b, activation="silu")
+    assert_close(out[real], rout, dtype)
+    assert_equal(st[ids[real].long()], rs)
+    untouched = [r for r in range(P) if r not in ids.tolist()]
+    assert_equal(st[untouched], pool[untouched])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 def test_strided_inputs(dtype):
     # x as a column slice, state with padded channel stride, transposed weight
