@@ -640,8 +640,17 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
                 ch.g[j] = row_load<T, CPL>(gb, (uint32_t)(t * gs2) * (uint32_t)sizeof(T) + lob);
             }
             if constexpr (SEQ) {
+                constexpr int NI = G + H;
+                if (ss1 == 1 && cs >= H && cs - H + NI <= L) {
+                    // the window's ids are consecutive and in range: one scalar load
+                    const __attribute__((address_space(4))) int32_t* q =
+                        (const __attribute__((address_space(4))) int32_t*)reinterpret_cast<uintptr_t>(sr + (cs - H));
 #pragma unroll
-                for (int i = 0; i < G + H; ++i) ch.ids[i] = ld_uniform(sr + clampL(cs - H + i) * ss1);
+                    for (int i = 0; i < NI; ++i) ch.ids[i] = q[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < NI; ++i) ch.ids[i] = ld_uniform(sr + clampL(cs - H + i) * ss1);
+                }
             }
         };
 
