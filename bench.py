@@ -91,6 +91,8 @@ def _parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target duration of each CPU-baseline leg")
     ap.add_argument("--settle", type=float, default=0.3,
                     help="seconds of untimed C2 kernels before the first timing (clock ramp)")
+    ap.add_argument("--kernel-settle", type=float, default=0.05,
+                    help="seconds of untimed replays of each per-kernel timing graph (clock ramp)")
     return ap.parse_args()
 
 
@@ -128,13 +130,21 @@ def _replay_times(torch, g, runs):
     return out
 
 
-def _time_launch_set(torch, fns, launches, runs):
+def _time_launch_set(torch, fns, launches, runs, settle):
     """Microseconds per launch, one value per run, of a graph of `launches` launches
-    cycling through the closures `fns` (one per rotating buffer set)."""
+    cycling through the closures `fns` (one per rotating buffer set), after `settle`
+    seconds of untimed replays: the host-side set-up between two cases leaves the GPU
+    idle, and for tens of ms after that it runs below its steady clocks (the C2
+    backward measured 48.6 us per launch straight after its set-up and 43.5 us after
+    50 ms of replays, in one process)."""
     def loop():
         for i in range(launches):
             fns[i % len(fns)]()
     g = _graph(torch, loop)
+    t_end = time.perf_counter() + settle
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
     us = [ms * 1e3 / launches for ms in _replay_times(torch, g, runs)]
     del g
     return us
@@ -468,9 +478,9 @@ def _varlen_case(torch, cc, c3info):
                               {"note": "gathers 8 x 3 rows of 4096 channels (197 KB each way): launch-bound"})}
 
 
-def _run_cases(torch, cases, launches, runs, res):
+def _run_cases(torch, cases, args, res):
     for name, (fns, nbytes, div, extra) in cases.items():
-        us = _time_launch_set(torch, fns, max(4, launches // div), runs)
+        us = _time_launch_set(torch, fns, max(4, args.launches // div), args.runs, args.kernel_settle)
         res[name] = _entry(us, nbytes, **extra)
         log(f"{name}: {res[name]['us_per_launch']} us/launch (min {res[name]['us_min']}, max {res[name]['us_max']}; "
             f"{res[name]['frac_of_peak']:.3f} of peak)")
@@ -480,7 +490,7 @@ def bench_configs(torch, cc, floors, args):
     """Every kernel at the other benchmark configurations (reported, not the headline)."""
     res = {}
     c3, c3info = _c3_cases(torch, floors)
-    _run_cases(torch, c3, args.launches, args.runs, res)
+    _run_cases(torch, c3, args, res)
     for name in ("c3a_bwd", "c3b_bwd", "c3a_bwd_typed", "c3b_bwd_typed"):
         if "floor_tiles256_c3" in res:
             res[name]["floor_same_pattern_us"] = res["floor_tiles256_c3"]["us_per_launch"]
@@ -488,11 +498,11 @@ def bench_configs(torch, cc, floors, args):
     del c3
     torch.cuda.empty_cache()
     c5 = _c5_cases(torch)
-    _run_cases(torch, c5, args.launches, args.runs, res)
+    _run_cases(torch, c5, args, res)
     del c5
     torch.cuda.empty_cache()
     c4b, hbm = _c4b_cases(torch, cc, floors)
-    _run_cases(torch, c4b, args.launches, args.runs, res)
+    _run_cases(torch, c4b, args, res)
     e = res["update_c4b"]
     e["us_per_call"] = e["us_per_launch"]
     if hbm:
@@ -505,7 +515,7 @@ def bench_configs(torch, cc, floors, args):
         e["floor_chunks2_us"] = res["floor_chunks2_c4b"]["us_per_launch"]
     del c4b
     torch.cuda.empty_cache()
-    _run_cases(torch, _varlen_case(torch, cc, c3info), args.launches, args.runs, res)
+    _run_cases(torch, _varlen_case(torch, cc, c3info), args, res)
     return res
 
 
@@ -649,8 +659,8 @@ def main():
     sets, w, b = _c2_sets(torch, nsets)
     ms = bench_step(torch, cc, args, sets, w, b)
     kern = {}
-    _run_cases(torch, _c2_cases(torch, sets, w, b), args.launches, args.runs, kern)
-    _run_cases(torch, _c2_floor_cases(torch, sets, floors), args.launches, args.runs, kern)
+    _run_cases(torch, _c2_cases(torch, sets, w, b), args, kern)
+    _run_cases(torch, _c2_floor_cases(torch, sets, floors), args, kern)
     for k in ("fwd", "bwd", "bwd_typed"):
         kern[k]["buffer_sets"] = nsets
     for k in ("bwd", "bwd_typed"):
@@ -658,7 +668,7 @@ def main():
         kern[k]["floor_streams_4rows_us"] = kern["floor_tiles1024_c2"]["us_per_launch"]
     del sets
     torch.cuda.empty_cache()
-    _run_cases(torch, _c4a_cases(torch, cc, floors), args.launches, args.runs, kern)
+    _run_cases(torch, _c4a_cases(torch, cc, floors), args, kern)
     u = kern["update_c4a"]
     u["us_per_call"] = u["us_per_launch"]
     u["us_per_call_cache_resident"] = kern.pop("update_c4a_cache_resident")["us_per_launch"]

@@ -642,7 +642,9 @@ namespace {
 constexpr int kLinNV = 2;
 // update_dir: batch entries per wavefront and dwords of x per lane. C4a (A/B
 // on one box, update_lin 7.14 us): 2 x 1 -> 6.97 us; 1 x 1 7.06; 4 x 1 7.03;
-// 2 x 2 7.38; 1 x 2 7.15; 1 x 4 7.48; 4 x 2 7.80. Without SiLU, or with the
+// 2 x 2 7.38; 1 x 2 7.15; 1 x 4 7.48; 4 x 2 7.80. Wider contiguous spans per
+// lane (2 or 4 dwords of x, 6 or 12 of state, so that one load instruction no
+// longer covers contiguous bytes): 7.50 / 8.05 us. Without SiLU, or with the
 // weights and bias replaced by constants, 2 x 1 measures the same 6.97-7.05 us:
 // what is left is the access pattern (a copy that moves the same bytes as
 // 16-byte vectors, one x and three state vectors per lane, takes ~0.4 us less).
