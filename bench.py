@@ -323,12 +323,17 @@ def _c2_cases(torch, sets, w, b):
 def _c2_floor_cases(torch, sets, floors):
     """The C2 backward's streams with no arithmetic: x and dout read, dx written, on the
     same sets viewed as (B * D) rows of 4 KB: a wavefront per 4 rows x 1 KB, or per row
-    (4 KB, the backward kernel's own item), 16 bytes per lane per load."""
+    (4 KB, the backward kernel's own item), 16 bytes per lane per load; and the forward's
+    streams (x read, out written) as a plain copy."""
     bufs = [(x.detach().reshape(B * D, L), dout.reshape(B * D, L), torch.empty(B * D, L, dtype=x.dtype,
                                                                                  device=x.device))
             for x, dout in sets]
-    return {f"floor_tiles{seg}_c2": ([lambda u=u, seg=seg: floors.tiles(torch, u[0], u[1], u[2], seg) for u in bufs],
-                                     3 * B * D * L * 2, 1, {}) for seg in (1024, 4096)}
+    cases = {f"floor_tiles{seg}_c2": ([lambda u=u, seg=seg: floors.tiles(torch, u[0], u[1], u[2], seg) for u in bufs],
+                                      3 * B * D * L * 2, 1, {}) for seg in (1024, 4096)}
+    # the forward's streams: x read, out written, one 16-byte vector per lane
+    cases["floor_copy_c2"] = ([lambda u=u: floors.copy(torch, u[0], u[2]) for u in bufs], 2 * B * D * L * 2, 1,
+                              {"note": "plain copy of x into out (the forward's bytes), no arithmetic"})
+    return cases
 
 
 def _update_sets(torch, n, seqlen=1, S=W - 1, seed=7):
@@ -663,6 +668,7 @@ def main():
     _run_cases(torch, _c2_floor_cases(torch, sets, floors), args, kern)
     for k in ("fwd", "bwd", "bwd_typed"):
         kern[k]["buffer_sets"] = nsets
+    kern["fwd"]["floor_copy_us"] = kern["floor_copy_c2"]["us_per_launch"]
     for k in ("bwd", "bwd_typed"):
         kern[k]["floor_same_streams_us"] = kern["floor_tiles4096_c2"]["us_per_launch"]
         kern[k]["floor_streams_4rows_us"] = kern["floor_tiles1024_c2"]["us_per_launch"]
