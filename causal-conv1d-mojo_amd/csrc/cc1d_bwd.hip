@@ -569,15 +569,6 @@ template <typename T, int CPL> __device__ __forceinline__ void row_store_nt(T* b
     __builtin_nontemporal_store(v.d[0], reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(base) + off));
 }
 
-// A copy of a lane's raw row that the compiler cannot see through: the
-// widening of a row is then done in the step that uses it, not for a whole
-// chunk at once (which kept twice the chunk's registers live).
-template <typename T, int CPL> __device__ __forceinline__ Lanes<T, CPL> pinned(Lanes<T, CPL> v) {
-    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
-    asm volatile("" : "+v"(v.d[0]));
-    return v;
-}
-
 // Kernel: the WPB wavefronts of a block take WPB consecutive runs of the same
 // channels; their weight/bias-gradient partials are summed through LDS and
 // the block adds the sums with fp32 atomics on consecutive addresses (or
@@ -667,12 +658,17 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
         Chunk A, B;
         load(t0, A, std::integral_constant<int, G>{});
 
-        float w[W][CPL], bias[CPL];
+        // w for dx; wq, bq (scaled by -log2(e)) give the SiLU argument q = -log2(e) * pre
+        // directly, as the exponent silu_bwd_q takes
+        float w[W][CPL], wq[W][CPL], bq[CPL];
 #pragma unroll
         for (int e = 0; e < CPL; ++e) {
 #pragma unroll
-            for (int k = 0; k < W; ++k) w[k][e] = to_f32(wt.w[k][e]);
-            bias[e] = wt.bias(e);
+            for (int k = 0; k < W; ++k) {
+                w[k][e] = to_f32(wt.w[k][e]);
+                wq[k][e] = -kLog2e * w[k][e];
+            }
+            bq[e] = -kLog2e * wt.bias(e);
         }
 #pragma unroll
         for (int k = 0; k < H; ++k) {
@@ -726,18 +722,18 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
                 float xc[CPL], dn[CPL], o[CPL];
-                const Lanes<T, CPL> xl = pinned(ch.x[j]), gl = pinned(ch.g[j]);
+                const Lanes<T, CPL> xl = ch.x[j], gl = ch.g[j];
 #pragma unroll
                 for (int e = 0; e < CPL; ++e) {
                     xc[e] = xl.get(e);
                     const float gval = gl.get(e);
                     float d = gval;
                     if constexpr (SILU) {
-                        float pre = bias[e];
+                        float q = bq[e];
 #pragma unroll
-                        for (int k = 0; k < H; ++k) pre = __builtin_fmaf(w[k][e], s.xw[k][e], pre);
-                        pre = __builtin_fmaf(w[H][e], xc[e], pre);
-                        d = silu_bwd_q(gval, -kLog2e * pre);
+                        for (int k = 0; k < H; ++k) q = __builtin_fmaf(wq[k][e], s.xw[k][e], q);
+                        q = __builtin_fmaf(wq[H][e], xc[e], q);
+                        d = silu_bwd_q(gval, q);
                     }
                     dn[e] = d;
                     if constexpr (ACC) {
@@ -779,19 +775,19 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
                 }
                 const bool dead = !in || idp < 0;
                 float xc[CPL], dn[CPL];
-                const Lanes<T, CPL> xl = pinned(ch.x[j]), gl = pinned(ch.g[j]);
+                const Lanes<T, CPL> xl = ch.x[j], gl = ch.g[j];
 #pragma unroll
                 for (int e = 0; e < CPL; ++e) {
                     xc[e] = in ? xl.get(e) : 0.0f;
                     const float gval = gl.get(e);
                     float d = gval;
                     if constexpr (SILU) {
-                        float pre = bias[e];
+                        float q = bq[e];
 #pragma unroll
                         for (int k = 0; k < H; ++k)
-                            if (idk[k] == idp) pre = __builtin_fmaf(w[k][e], s.xw[k][e], pre);
-                        pre = __builtin_fmaf(w[H][e], xc[e], pre);
-                        d = silu_bwd_q(gval, -kLog2e * pre);
+                            if (idk[k] == idp) q = __builtin_fmaf(wq[k][e], s.xw[k][e], q);
+                        q = __builtin_fmaf(wq[H][e], xc[e], q);
+                        d = silu_bwd_q(gval, q);
                     }
                     if (dead) d = 0.0f;
                     dn[e] = d;
