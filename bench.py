@@ -185,7 +185,9 @@ class Floors:
         lib.cc1d_floor_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
         lib.cc1d_floor_chunks.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, vp]
         lib.cc1d_floor_tiles.argtypes = [vp, vp, vp, i64, i64, i32, vp]
-        for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks, lib.cc1d_floor_tiles):
+        lib.cc1d_floor_walk.argtypes = [vp, vp, vp, i64, i64, vp]
+        for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks, lib.cc1d_floor_tiles,
+                  lib.cc1d_floor_walk):
             f.restype = i32
         self.lib = lib
 
@@ -210,6 +212,12 @@ class Floors:
         self._check(self.lib.cc1d_floor_tiles(x.data_ptr(), g.data_ptr(), out.data_ptr(), x.shape[0],
                                               x.shape[1] * x.element_size(), seg,
                                               torch.cuda.current_stream().cuda_stream), "cc1d_floor_tiles")
+
+    def walk(self, torch, x, g, out):
+        """x, g, out: (rows, row) tensors, contiguous rows; rows a multiple of 1024"""
+        self._check(self.lib.cc1d_floor_walk(x.data_ptr(), g.data_ptr(), out.data_ptr(), x.shape[0],
+                                             x.shape[1] * x.element_size(), torch.cuda.current_stream().cuda_stream),
+                    "cc1d_floor_walk")
 
     def chunks(self, torch, x, out, pool, idx, cs, nchunks):
         line_chunks = pool.shape[2] * pool.element_size() // 16
@@ -428,6 +436,13 @@ def _c3_cases(torch, floors=None):
                 torch, x.transpose(1, 2)[0], d.transpose(1, 2)[0], dx.transpose(1, 2)[0], seg)
                 for x, d, _, dx in sets]
             cases[f"floor_tiles{seg}_c3"] = (fns, 3 * n3, 1, {})
+        # the backward's own walk (128-row runs of 256-byte slices, 4-row chunks) without arithmetic
+        fns = [lambda x=x, d=d, dx=dx: floors.walk(torch, x.transpose(1, 2)[0], d.transpose(1, 2)[0],
+                                                   dx.transpose(1, 2)[0]) for x, d, _, dx in sets]
+        cases["floor_walk_c3"] = (fns, 3 * n3, 1, {"note": "bwd_clw's walk, grid and blocks, no arithmetic"})
+        # the forward's streams: x read, out written, as a plain copy
+        fns = [lambda x=x, o=o: floors.copy(torch, x.transpose(1, 2), o.transpose(1, 2)) for x, _, o, _ in sets]
+        cases["floor_copy_c3"] = (fns, 2 * n3, 1, {"note": "plain copy of x into out (the forward's bytes)"})
     return cases, (cuts, L3, D3)
 
 
@@ -500,6 +515,10 @@ def bench_configs(torch, cc, floors, args):
         if "floor_tiles256_c3" in res:
             res[name]["floor_same_pattern_us"] = res["floor_tiles256_c3"]["us_per_launch"]
             res[name]["floor_widest_pattern_us"] = res["floor_tiles1024_c3"]["us_per_launch"]
+            res[name]["floor_walk_us"] = res["floor_walk_c3"]["us_per_launch"]
+    for name in ("c3a_fwd", "c3b_fwd"):
+        if "floor_copy_c3" in res:
+            res[name]["floor_copy_us"] = res["floor_copy_c3"]["us_per_launch"]
     del c3
     torch.cuda.empty_cache()
     c5 = _c5_cases(torch)

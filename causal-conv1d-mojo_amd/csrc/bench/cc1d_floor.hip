@@ -23,6 +23,11 @@
 //                        last kernel's shape; seg 1024: 16 bytes per lane, 4
 //                        rows; seg 4096: 4 x 16 bytes per lane, one row, the
 //                        channel-first kernel's shape).
+//   cc1d_floor_walk   -- the channel-last backward's walk: x and g read, out
+//                        = x ^ g ^ 1 written, a wavefront walking 128 rows of
+//                        a 256-byte column slice in 4-row chunks with the
+//                        next chunk's loads in flight (bwd_clw's loop, its
+//                        grid and block shape, no arithmetic).
 //   cc1d_floor_chunks -- the circular decode update's pattern: per (b, c),
 //                        read and write back `chunks` consecutive 16-byte
 //                        chunks of state line (idx[b], c) starting at chunk
@@ -128,6 +133,52 @@ __global__ void __launch_bounds__(256) floor_tiles(const char* __restrict__ x, c
                                         reinterpret_cast<V*>(out + base + r * row_bytes + v * 64 * NB));
 }
 
+// The channel-last backward's walk without its arithmetic: a wavefront walks
+// R consecutive rows of a 256-byte column slice (a dword per lane) in G-row
+// chunks, the next chunk's loads issued before the current one's stores
+// (two chunk buffers), a scheduling fence after each row; WPB wavefronts per
+// block take consecutive runs of one slice (grid: slices fastest, then run
+// groups), as bwd_clw's blocks do.
+template <int G, int R, int WPB>
+__global__ void __launch_bounds__(64 * WPB) floor_walk(const char* __restrict__ x, const char* __restrict__ g,
+                                                       char* __restrict__ out, uint32_t row_bytes, uint32_t nslice) {
+    constexpr int NCH = R / G;
+    static_assert(R % (2 * G) == 0, "chunks in pairs");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t slice = __builtin_amdgcn_readfirstlane(blockIdx.x % nslice);
+    const uint32_t run = __builtin_amdgcn_readfirstlane(blockIdx.x / nslice) * WPB + wave;
+    const size_t base = (size_t)run * R * row_bytes + slice * 256;
+    const char* xb = x + base;
+    const char* gb = g + base;
+    char* ob = out + base;
+    const uint32_t lo = lane * 4;
+    uint32_t cx[2][G], cg[2][G];
+    auto load = [&](int c, int buf) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const uint32_t off = (uint32_t)(c * G + j) * row_bytes + lo;
+            cx[buf][j] = *reinterpret_cast<const uint32_t*>(xb + off);
+            cg[buf][j] = *reinterpret_cast<const uint32_t*>(gb + off);
+        }
+    };
+    auto rows = [&](int c, int buf) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const uint32_t off = (uint32_t)(c * G + j) * row_bytes + lo;
+            __builtin_nontemporal_store(cx[buf][j] ^ cg[buf][j] ^ 1u, reinterpret_cast<uint32_t*>(ob + off));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    load(0, 0);
+#pragma unroll 1
+    for (int c = 0; c < NCH; c += 2) {
+        load(c + 1, 1);
+        rows(c, 0);
+        if (c + 2 < NCH) load(c + 2, 0);
+        rows(c + 1, 1);
+    }
+}
+
 bool launched() { return hipGetLastError() == hipSuccess; }
 
 }  // namespace
@@ -188,6 +239,23 @@ int cc1d_floor_tiles(const void* x, const void* g, void* out, int64_t rows, int6
     if (seg == 256) floor_tiles<4, 1, 16><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
     else if (seg == 1024) floor_tiles<16, 1, 4><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
     else floor_tiles<16, 4, 1><<<dim3((unsigned)blocks), 256, 0, s>>>(xc, gc, oc, row_bytes, nslice);
+    return launched() ? 0 : -2;
+}
+
+// x, g, out: `rows` rows of row_bytes each (4-byte aligned); row_bytes a
+// multiple of 256 below 2^32 / 128, rows a multiple of 1024 (8 runs of 128)
+int cc1d_floor_walk(const void* x, const void* g, void* out, int64_t rows, int64_t row_bytes, void* stream) {
+    constexpr int G = 4, R = 128, WPB = 8;
+    if (rows < 0 || row_bytes <= 0 || row_bytes % 256 || row_bytes * R >= ((int64_t)1 << 32) || rows % (R * WPB))
+        return -1;
+    if (rows == 0) return 0;
+    if (x == nullptr || g == nullptr || out == nullptr) return -1;
+    const int64_t nslice = row_bytes / 256;
+    const int64_t blocks = nslice * (rows / (R * WPB));
+    if (blocks >= ((int64_t)1 << 31)) return -1;
+    floor_walk<G, R, WPB><<<dim3((unsigned)blocks), 64 * WPB, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const char*>(x), static_cast<const char*>(g), static_cast<char*>(out), (uint32_t)row_bytes,
+        (uint32_t)nslice);
     return launched() ? 0 : -2;
 }
 

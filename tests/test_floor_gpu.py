@@ -86,3 +86,16 @@ def test_tiles_floor(floors, seg):
     want = x[:rows].view(torch.int32) ^ d[:rows].view(torch.int32) ^ 1  # bit patterns (some are NaNs)
     assert torch.equal(out[:rows].view(torch.int32), want)
     assert torch.all(out[rows:].view(torch.int16) == 0)
+
+
+def test_walk_floor(floors):
+    rows, width = 2048, 384  # bf16 rows of 768 bytes: 3 slices, 2 blocks of 8 runs per slice
+    g = torch.Generator(device=DEV).manual_seed(3)
+    x = torch.randn(rows + 5, width, generator=g, device=DEV).bfloat16()
+    d = torch.randn(rows + 5, width, generator=g, device=DEV).bfloat16()
+    out = torch.zeros_like(x)
+    floors.walk(torch, x[:rows], d[:rows], out[:rows])
+    torch.cuda.synchronize()
+    want = x[:rows].view(torch.int32) ^ d[:rows].view(torch.int32) ^ 1
+    assert torch.equal(out[:rows].view(torch.int32), want)
+    assert torch.all(out[rows:].view(torch.int16) == 0)
