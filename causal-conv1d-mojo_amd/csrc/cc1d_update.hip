@@ -15,7 +15,8 @@
 //                     x / out and contiguous state rows: a lane owns one dword
 //                     of x (2 bf16/fp16 channels, 1 fp32) of two batch
 //                     entries and loads the channels' state span (H dwords)
-//                     directly, one load per span; no LDS.
+//                     directly, one load per span; no LDS; four wavefronts
+//                     (channel groups) per workgroup.
 //   update_lin     -- the same for W > 5: one token, S == W-1, channel-contiguous x /
 //                     out and contiguous state rows: one wavefront per (batch
 //                     entry, 16 * EPV channels) moves the group's state and x
@@ -282,21 +283,23 @@ __global__ void __launch_bounds__(64) update_lin(const LinArgs<T> a) {
 // consecutive lanes hold consecutive spans, so each load instruction covers
 // 64 * 4H contiguous bytes. No LDS and no shuffle between the loads, the
 // arithmetic and the stores. A wavefront takes 64 * NS * CPL channels of BPW
-// batch entries (grid: channel groups x batch-entry groups); x first, then
+// batch entries, a workgroup WPG consecutive channel groups of the same
+// entries (grid: workgroups along the channels x batch-entry groups); x first, then
 // the BPW pool indices (scalar loads) behind a scheduling fence, then the
 // state spans, then the weights and bias (cache-resident), all before any
 // arithmetic.
-template <typename T, int W, int BPW, int NS, bool SILU, bool HAS_BIAS, bool HAS_IDX>
-__global__ void __launch_bounds__(64) update_dir(const LinArgs<T> a) {
+template <typename T, int W, int BPW, int NS, int WPG, bool SILU, bool HAS_BIAS, bool HAS_IDX>
+__global__ void __launch_bounds__(64 * WPG) update_dir(const LinArgs<T> a) {
     constexpr int H = W - 1;
     constexpr int CPL = 4 / (int)sizeof(T);
     static_assert(H >= 1 && H <= 4, "one dword vector of state per span");
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const uint32_t grp = blockIdx.x * WPG + (threadIdx.x >> 6);  // channel group of this wavefront
     uint32_t c[NS];
     bool on[NS];
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
-        const uint32_t cu = (blockIdx.x * (64 * NS) + 64 * u + lane) * CPL;
+        const uint32_t cu = (grp * (64 * NS) + 64 * u + lane) * CPL;
         on[u] = cu < a.dim;
         c[u] = on[u] ? cu : 0;  // lanes past the end read channel 0 and store nothing
     }
@@ -650,6 +653,12 @@ constexpr int kLinNV = 2;
 // 16-byte vectors, one x and three state vectors per lane, takes ~0.4 us less).
 constexpr int kDirBPW = 2;
 constexpr int kDirNS = 1;
+// update_dir: wavefronts (consecutive channel groups) per workgroup. C4a, with
+// 2 batch entries per wavefront (one A/B session): 1 -> 6.96-6.97 us, 2 ->
+// 6.81-6.82, 4 -> 6.76-6.78, 8 -> 7.07-7.08; 1 entry x 4 wavefronts 7.55,
+// 4 entries x 4 wavefronts 7.08. The scattered-row copy does not gain from
+// wider workgroups (6.50 us with 1, 6.53 with 2, 4 or 5 wavefronts).
+constexpr int kDirWPG = 4;
 
 template <typename T>
 bool lin_ok(const cc1d_update_params& p) {
@@ -725,11 +734,12 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                     la.nbatch = (uint32_t)p.batch;
                     if constexpr (W - 1 <= 4) {
                         constexpr int CPL = 4 / (int)sizeof(T);
-                        const dim3 gd((unsigned)ceil_div(p.dim, 64 * kDirNS * CPL), (unsigned)ceil_div(p.batch, kDirBPW));
+                        const dim3 gd((unsigned)ceil_div(ceil_div(p.dim, 64 * kDirNS * CPL), kDirWPG),
+                                      (unsigned)ceil_div(p.batch, kDirBPW));
                         return with_flag(p.bias != nullptr, [&](auto hb) {
                             return with_flag(p.conv_state_indices != nullptr, [&](auto hi) {
-                                update_dir<T, W, kDirBPW, kDirNS, SILU, decltype(hb)::value, decltype(hi)::value>
-                                    <<<gd, 64, 0, stream>>>(la);
+                                update_dir<T, W, kDirBPW, kDirNS, kDirWPG, SILU, decltype(hb)::value, decltype(hi)::value>
+                                    <<<gd, 64 * kDirWPG, 0, stream>>>(la);
                                 return launch_status();
                             });
                         });
