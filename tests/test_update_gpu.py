@@ -37,7 +37,8 @@ def _run(x, state, w, b=None, **kw):
 @pytest.mark.parametrize("width", [2, 3, 4, 5, 9])
 @pytest.mark.parametrize("activation", [None, "silu"])
 @pytest.mark.parametrize("has_bias", [True, False], ids=["bias", "nobias"])
-@pytest.mark.parametrize("dim", [16, 40, 2048])
+# 1400: 11 channel groups of 128 bf16 channels, the last one partial, in workgroups of 4 groups
+@pytest.mark.parametrize("dim", [16, 40, 1400, 2048])
 def test_single_token(dtype, width, activation, has_bias, dim):
     x, w, b, _ = make_inputs(3, dim, 1, width, dtype=dtype, has_bias=has_bias)
     state = make_inputs(3, dim, width - 1, width, dtype=dtype, seed=1)[0]
