@@ -1,10 +1,14 @@
 // cc1d_floor.hip -- bandwidth floors for bench.py (measurement only; the
 // product library does not contain or call these kernels).
 //
-// Each kernel moves the bytes of one decode-update configuration with no
-// arithmetic, so its time is what HBM and the launch cost for that access
-// pattern on this GPU. Every store writes a value that differs from what was
-// loaded (bits flipped), so no store can be dropped as a no-op.
+// Each kernel moves the bytes of one configuration with no arithmetic, so
+// its time is what HBM and the launch cost for that access pattern on this
+// GPU. Every store writes a value that differs from what was loaded (bits
+// flipped), so no store can be dropped as a no-op. Every access that is not a
+// partial-line read-modify-write is non-temporal: on this GPU that is the
+// faster form for data touched once (the C2 one-row-per-wavefront streams
+// 40.2 against 43.4 us with cached loads, the C4a scattered rows 5.2 against
+// 6.5 us); the circular decode's state chunks stay cached, as in the kernel.
 //
 //   cc1d_floor_copy   -- a plain streaming copy of n 16-byte vectors: one
 //                        vector per lane, 64-thread blocks (the fastest shape
@@ -49,7 +53,7 @@ __device__ __forceinline__ u32x4 flip(u32x4 v) {
 
 __global__ void __launch_bounds__(64) floor_copy(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
-    if (i < n) dst[i] = flip(src[i]);
+    if (i < n) __builtin_nontemporal_store(flip(__builtin_nontemporal_load(&src[i])), &dst[i]);
 }
 
 // one wavefront per (entry, group of 64 x vectors): lane l moves x vector l
@@ -69,18 +73,18 @@ __global__ void __launch_bounds__(64) floor_rows(const u32x4* __restrict__ x, u3
     const uint32_t b = blockIdx.y;
     const uint32_t g = blockIdx.x;
     const uint32_t xi = min(g * 64 + lane, xvec - 1);
-    const u32x4 xv = x[(size_t)b * xvec + xi];
+    const u32x4 xv = __builtin_nontemporal_load(&x[(size_t)b * xvec + xi]);
     __builtin_amdgcn_sched_barrier(0);
     const int32_t r = *(const __attribute__((address_space(4))) int32_t*)(idx + b);
     u32x4* sr = pool + (size_t)(r >= 0 && r < pool_rows ? r : 0) * pool_row_vec + g * 64 * R;
     const uint32_t nsv = (xvec - g * 64) * R;  // state vectors left in this row from the group's start
     u32x4 sv[R];
 #pragma unroll
-    for (int j = 0; j < R; ++j) sv[j] = sr[min((uint32_t)(j * 64 + lane), nsv - 1)];
+    for (int j = 0; j < R; ++j) sv[j] = __builtin_nontemporal_load(&sr[min((uint32_t)(j * 64 + lane), nsv - 1)]);
     __builtin_amdgcn_sched_barrier(0);
-    out[(size_t)b * xvec + xi] = flip(xv);
+    __builtin_nontemporal_store(flip(xv), &out[(size_t)b * xvec + xi]);
 #pragma unroll
-    for (int j = 0; j < R; ++j) sr[min((uint32_t)(j * 64 + lane), nsv - 1)] = flip(sv[j]);
+    for (int j = 0; j < R; ++j) __builtin_nontemporal_store(flip(sv[j]), &sr[min((uint32_t)(j * 64 + lane), nsv - 1)]);
 }
 
 __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__ x, uint32_t* __restrict__ out,
@@ -93,7 +97,7 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
     const int64_t b = t / dim;
     const int64_t c = t - b * dim;
     uint32_t xv[4];
-    for (int i = 0; i < xwords; ++i) xv[i] = x[t * xwords + i];
+    for (int i = 0; i < xwords; ++i) xv[i] = __builtin_nontemporal_load(&x[t * xwords + i]);
     const int32_t row = idx[b];
     if (row < 0 || row >= pool_rows) return;
     int64_t k = cs[b] % line_chunks;
@@ -101,7 +105,7 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
     u32x4* line = pool + (int64_t)row * pool_row_chunks + c * line_chunks;
     u32x4 v[2];
     for (int j = 0; j < chunks; ++j) v[j] = line[(k + j) % line_chunks];
-    for (int i = 0; i < xwords; ++i) out[t * xwords + i] = xv[i] ^ 1u;
+    for (int i = 0; i < xwords; ++i) __builtin_nontemporal_store(xv[i] ^ 1u, &out[t * xwords + i]);
     for (int j = 0; j < chunks; ++j) line[(k + j) % line_chunks] = flip(v[j]);
 }
 
@@ -122,8 +126,8 @@ __global__ void __launch_bounds__(256) floor_tiles(const char* __restrict__ x, c
     for (int r = 0; r < ROWS; ++r)
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
-            xv[r][v] = *reinterpret_cast<const V*>(x + base + r * row_bytes + v * 64 * NB);
-            gv[r][v] = *reinterpret_cast<const V*>(g + base + r * row_bytes + v * 64 * NB);
+            xv[r][v] = __builtin_nontemporal_load(reinterpret_cast<const V*>(x + base + r * row_bytes + v * 64 * NB));
+            gv[r][v] = __builtin_nontemporal_load(reinterpret_cast<const V*>(g + base + r * row_bytes + v * 64 * NB));
         }
 #pragma unroll
     for (int r = 0; r < ROWS; ++r)
@@ -157,8 +161,8 @@ __global__ void __launch_bounds__(64 * WPB) floor_walk(const char* __restrict__ 
 #pragma unroll
         for (int j = 0; j < G; ++j) {
             const uint32_t off = (uint32_t)(c * G + j) * row_bytes + lo;
-            cx[buf][j] = *reinterpret_cast<const uint32_t*>(xb + off);
-            cg[buf][j] = *reinterpret_cast<const uint32_t*>(gb + off);
+            cx[buf][j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(xb + off));
+            cg[buf][j] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(gb + off));
         }
     };
     auto rows = [&](int c, int buf) {

@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(64 * WPG) update_dir(const LinArgs<T> a) {
         const uint32_t b = min(b0 + q, nb - 1);
 #pragma unroll
         for (int u = 0; u < NS; ++u)
-            xd[q][u] = *reinterpret_cast<const uint32_t*>(a.x + (size_t)b * a.x_row + c[u]);
+            xd[q][u] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(a.x + (size_t)b * a.x_row + c[u]));
     }
     // the pool indices (scalar loads) after the index-free x loads; the fence
     // keeps the compiler from hoisting them and their wait above those
@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(64 * WPG) update_dir(const LinArgs<T> a) {
         for (int u = 0; u < NS; ++u) {
             const uint32_t* sp = reinterpret_cast<const uint32_t*>(srow + (size_t)c[u] * H);
 #pragma unroll
-            for (int i = 0; i < H; ++i) st[q][u][i] = sp[i];
+            for (int i = 0; i < H; ++i) st[q][u][i] = __builtin_nontemporal_load(&sp[i]);
         }
     }
     // weights and bias (cache-resident) after the state loads: they arrive
@@ -397,13 +397,13 @@ __global__ void __launch_bounds__(64 * WPG) update_dir(const LinArgs<T> a) {
             else od = pack2<T>(o[0], o[1]);
             if (row[q] < 0) od = 0u;  // padding entry: zero output, state untouched
             if (on[u] && b0 + q < nb) {  // (an entry past the batch computed on clamped data)
-                *reinterpret_cast<uint32_t*>(a.out + (size_t)(b0 + q) * a.out_row + c[u]) = od;
+                __builtin_nontemporal_store(od, reinterpret_cast<uint32_t*>(a.out + (size_t)(b0 + q) * a.out_row + c[u]));
                 if (row[q] >= 0) {
                     uint32_t* sp = reinterpret_cast<uint32_t*>(a.conv_state + (size_t)row[q] * a.state_row +
                                                                (size_t)c[u] * H);
 #pragma unroll
                     for (int i = 0; i < H; ++i)
-                        sp[i] = CPL == 1 ? nraw[i] : (nraw[2 * i] | (nraw[2 * i + 1] << 16));
+                        __builtin_nontemporal_store(CPL == 1 ? nraw[i] : (nraw[2 * i] | (nraw[2 * i + 1] << 16)), &sp[i]);
                 }
             }
         }
@@ -546,7 +546,7 @@ __device__ __forceinline__ void update_circ_chunks(const cc1d_update_params& p, 
                 uint32_t v;
                 if constexpr (PER == 1) v = __float_as_uint(o[d]);
                 else v = pack2<T>(o[2 * d], o[2 * d + 1 < LMAX ? 2 * d + 1 : 0]);
-                reinterpret_cast<uint32_t*>(orow)[d] = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<uint32_t*>(orow) + d);
             }
         }
     }
@@ -580,7 +580,7 @@ __global__ void __launch_bounds__(256) update_circ_vec(const UpdArgs a) {
         constexpr int PER = 4 / (int)sizeof(T);
 #pragma unroll
         for (int d = 0; d < (LMAX + PER - 1) / PER; ++d) {
-            const uint32_t v = d * PER < Ls ? reinterpret_cast<const uint32_t*>(xr)[d] : 0u;
+            const uint32_t v = d * PER < Ls ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(xr) + d) : 0u;
 #pragma unroll
             for (int e = 0; e < PER; ++e)
                 if (d * PER + e < LMAX) xb[d * PER + e] = PER == 1 ? v : ((v >> (16 * e)) & 0xffffu);
