@@ -205,10 +205,6 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                     }
                 }
             }
-            // one vector at a time: otherwise the neighbour-lane halos of every vector
-            // are fetched up front, which waits for nearly the whole tile's loads
-            // before the first vector's arithmetic (C2: 44.1-44.2 against 44.4 us)
-            __builtin_amdgcn_sched_barrier(0);
         }
 
         // ---- dpre of the first H positions of the next segment (used by lane 63;
@@ -301,7 +297,6 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                 }
             }
             if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
-            __builtin_amdgcn_sched_barrier(0);
         }
 
         // ---- dinitial_states (bwd_full_cpu/kernel.mojo:210-219) ----
