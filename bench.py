@@ -71,7 +71,7 @@ C4B_S = 64
 C4B_BYTES = UPD_B * D * (8 + 6 + 8 + 8) + D * W * 2 + D * 2 + 2 * UPD_B * 4  # 39,374,848
 C4B_LINE_BYTES = UPD_B * D * 128  # whole 128-byte state lines under the touched chunks
 
-FLOOR_LIB = ROOT / "causal-conv1d-mojo_amd" / "causal_conv1d_amd" / "_lib" / "libcc1d_floor.so"
+FLOOR_LIB = ROOT / "libcc1d_floor.so"  # built by csrc/build.py from csrc/bench/cc1d_floor.hip
 
 
 def log(msg):

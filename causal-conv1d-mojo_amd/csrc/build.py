@@ -4,8 +4,9 @@ Each ``*.hip`` translation unit in this directory is compiled to an object
 with hipcc (in parallel), then linked into
 ``causal_conv1d_amd/_lib/libcc1d_amd.so``. The library exposes only the
 ``extern "C"`` entry points of ``include/cc1d.h``. ``bench/cc1d_floor.hip``
-(bandwidth floors that ``bench.py`` times beside the kernels) is linked on
-its own into ``causal_conv1d_amd/_lib/libcc1d_floor.so``.
+(bandwidth floors that ``bench.py`` times beside the kernels; measurement
+code, not part of the package) is linked on its own into
+``libcc1d_floor.so`` beside ``bench.py`` at the repository root.
 
 Usage: ``python causal-conv1d-mojo_amd/csrc/build.py [--jobs N] [--verbose]``.
 """
@@ -27,9 +28,9 @@ INCLUDE = REPO / "include"
 OBJ_DIR = CSRC / "_build"
 LIB_DIR = PKG_ROOT / "causal_conv1d_amd" / "_lib"
 LIB_PATH = LIB_DIR / "libcc1d_amd.so"
-# bandwidth floors for bench.py (measurement only; not part of the product library)
+# bandwidth floors for bench.py (measurement only: built beside bench.py, outside the package)
 FLOOR_SRC = CSRC / "bench" / "cc1d_floor.hip"
-FLOOR_PATH = LIB_DIR / "libcc1d_floor.so"
+FLOOR_PATH = REPO / "libcc1d_floor.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")

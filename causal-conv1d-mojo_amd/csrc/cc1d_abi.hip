@@ -48,8 +48,8 @@ int bwd_typed_entry(const cc1d_bwd_params* p, const cc1d_bwd_grads* g, void* str
     if (!grid_fits(p->batch * p->dim * p->seqlen)) return CC1D_ERR_SHAPE;
     if (p->x == nullptr || p->weight == nullptr || p->dout == nullptr || p->dx == nullptr)
         return CC1D_ERR_NULL_POINTER;
+    // (a NULL workspace is refused by the launcher when the call needs one)
     if (noalloc) return launch_bwd_typed_noalloc(*p, *g, s);
-    if (g->workspace == nullptr) return CC1D_ERR_NULL_POINTER;
     return launch_bwd_typed(*p, *g, s);
 }
 

@@ -1,1197 +1,26 @@
-// cc1d_bwd.hip -- fused backward kernels for gfx950.
-//
-// Semantics (src/causal_conv1d_mojo/bwd_full_cpu/kernel.mojo:25-314):
-//   dpre[t] = dout[t] * silu'(pre[t]) (or dout[t] without SiLU); 0 for t
-//             outside [0, L) and where seq_idx[t] < 0; pre is recomputed
-//             exactly as in the forward.
-//   dx[t]   = sum_k w[W-1-k] * dpre[t+k], tap k kept when seq_idx[t+k] == seq_idx[t]
-//   dw[k]  += sum_t dpre[t] * xx(t+k-(W-1)), same gate as the forward
-//   db     += sum_t dpre[t]
-//   dinit[i] = sum_{k<=i} w[k] * dpre[i-k]   (i < W-1)
-// dweight/dbias are reduced in fp32: per lane, then across the wavefront
-// (row kernels: DPP adds) or the block (channel-last: LDS).
-// cc1d_bwd adds the sums into the caller's zeroed fp32 accumulators with
-// atomics -- as in the reference, the order of those adds (over batches and
-// segments) is not fixed. cc1d_bwd_typed writes them as partial records
-// instead, and bwd_reduce adds each channel's records in a fixed order
-// (several records in flight per wavefront) and rounds once to the dtype.
-//
-// Kernels
-//   bwd_rows_vec -- channel-first rows, same lane layout and item order as
-//                   fwd_rows_vec (one item per wavefront, 4 per block).
-//   bwd_clw      -- channel-last (unit channel stride); a lane owns 4 bytes of
-//                   adjacent channels, a wavefront walks a run of time steps.
-//   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
+// cc1d_bwd.hip -- backward entry points: dispatch on the dtype code to the
+// per-dtype launchers (cc1d_bwd_kernels.hpp, instantiated by
+// cc1d_bwd_{fp16,bf16,fp32}.hip), and the allocation-free typed backward
+// with its static device scratch.
 #include <mutex>
 
 #include "cc1d_internal.hpp"
 
 namespace cc1d {
 
-struct BwdArgs {
-    cc1d_bwd_params p;
-    float* part;      // non-null: write weight/bias-gradient partial sums here instead of atomics
-    int64_t nseg;     // rows_vec: segments per row; cl: run groups per row; generic: chunks per row
-    int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
-    int64_t chunk;    // cl: time steps per run; generic: time steps per thread
-    int64_t groups;   // cl: channel groups of 64 * CPL
-};
-
-// channel-first rows: (row, segment) items per block, one per wavefront
-constexpr int kRowsWPB = 4;
-// channel-last walk: time steps per chunk, per wavefront run, runs per block
-constexpr int kClG = 4;
-constexpr int kClR = 128;
-constexpr int kClWPB = 8;
-
-// Registers of one wavefront-segment of a row: VPT 16-byte vectors of x and
-// dout per lane, plus the halos (lane 0: the vector of x before the segment;
-// lane 63: x and dout of the first vector after it).
-template <int VPT> struct RowTile {
-    u32x4 v[VPT], gv[VPT], h, xn, gn;
-};
-
-// Issue the loads of segment t0 of row (b, c). FULL: the whole segment lies
-// inside the row.
-template <typename T, int VPT, bool FULL>
-__device__ __forceinline__ void bwd_rows_load(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c, int32_t t0,
-                                              RowTile<VPT>& r) {
-    constexpr int EPV = elems16<T>::value;
-    constexpr int SEG = 64 * VPT * EPV;
-    const int32_t L = (int32_t)p.seqlen;
-    const int32_t tn = t0 + SEG;  // first position of the next segment
-    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
-    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int32_t t = t0 + (j * 64 + lane) * EPV;
-        r.v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
-        r.gv[j] = (FULL || t < L) ? vload_nt(gr + t) : vzero();
-    }
-    // halo vectors: wave-uniform reads at clamped (always valid) addresses
-    const u32x4 hv = vload_uniform(xr + (t0 > 0 ? t0 - EPV : 0));
-    const int32_t tq = tn < L ? tn : t0;
-    const u32x4 xv = vload_uniform(xr + tq), gq = vload_uniform(gr + tq);
-    r.h = (lane == 0 && t0 > 0) ? hv : vzero();
-    r.xn = (lane == 63 && tn < L) ? xv : vzero();
-    r.gn = (lane == 63 && tn < L) ? gq : vzero();
-}
-
-// One wavefront-segment of row (b, c) from its loaded tile: writes dx (and
-// dinitial_states) and adds this segment's weight/bias-gradient partials
-// into pw / pb.
-template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
-__device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0, const RowTile<VPT>& r, const float* w, const float* wq,
-                                                 float bq, float* pw, float& pb) {
-    constexpr int EPV = elems16<T>::value;
-    constexpr int H = W - 1;
-    constexpr int SEG = 64 * VPT * EPV;
-    static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
-    const int32_t L = (int32_t)p.seqlen;
-    {
-        const int32_t tn = t0 + SEG;  // first position of the next segment
-        T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
-        const auto& v = r.v;
-        const auto& gv = r.gv;
-        const u32x4 h = r.h, xn = r.xn, gn = r.gn;
-
-        int32_t id[VPT][EPV];
-        int32_t hid[H], nid[H];
-        if constexpr (SEQ) {
-            const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
-#pragma unroll
-            for (int j = 0; j < VPT; ++j) {
-                const int32_t t = t0 + (j * 64 + lane) * EPV;
-#pragma unroll
-                for (int q = 0; q < EPV / 4; ++q) {
-                    const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
-                                            : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                hid[i] = (lane == 0 && t0 - H + i >= 0) ? sr[t0 - H + i] : -1;
-                nid[i] = (lane == 63 && tn + i < L) ? sr[tn + i] : -1;
-            }
-        }
-
-        const bool init_row = p.initial_states != nullptr && t0 == 0;  // wave-uniform
-        const bool use_init = init_row && lane == 0;
-        float hinit[H];
-#pragma unroll
-        for (int i = 0; i < H; ++i) hinit[i] = 0.0f;
-        if (init_row) {
-            const T* is = static_cast<const T*>(p.initial_states) + b * p.initial_states_stride[0] +
-                          c * p.initial_states_stride[1];
-#pragma unroll
-            for (int i = 0; i < H; ++i) hinit[i] = ld_uniform(is + i * p.initial_states_stride[2]);
-        }
-        // dfinal_states of this row when the segment holds the row's end (wave-uniform)
-        float dfin[H];
-#pragma unroll
-        for (int i = 0; i < H; ++i) dfin[i] = 0.0f;
-        const bool dfin_row = p.dfinal_states != nullptr && tn >= L;
-        if (dfin_row) {
-            const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
-                           c * p.dfinal_states_stride[1];
-#pragma unroll
-            for (int i = 0; i < H; ++i) dfin[i] = ld_uniform(dfs + i * p.dfinal_states_stride[2]);
-        }
-
-        // ---- dpre for the owned positions + dweight/dbias partials ----
-        constexpr int D0 = ((EPV - H) * (int)sizeof(T)) / 4;
-        const int prev_lane = (lane + 63) & 63;
-        const int next_lane = (lane + 1) & 63;
-        float dp[VPT][EPV];
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int32_t t = t0 + (j * 64 + lane) * EPV;
-            u32x4 pv = vzero();
-#pragma unroll
-            for (int d = D0; d < 4; ++d) {
-                const uint32_t send = (lane == 63) ? (j > 0 ? v[j > 0 ? j - 1 : 0][d] : 0u) : v[j][d];
-                pv[d] = lane_get(send, prev_lane);
-            }
-            if (j == 0 && lane == 0) pv = h;
-            float win[H + EPV];
-#pragma unroll
-            for (int i = 0; i < H; ++i) win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
-#pragma unroll
-            for (int i = 0; i < EPV; ++i) win[H + i] = vget<T>(v[j], i);
-            int32_t sw[H + EPV];
-            if constexpr (SEQ) {
-#pragma unroll
-                for (int i = 0; i < H; ++i) {
-                    const int32_t send = (lane == 63) ? (j > 0 ? id[j > 0 ? j - 1 : 0][EPV - H + i] : -1)
-                                                      : id[j][EPV - H + i];
-                    const int32_t r = lane_get(send, prev_lane);
-                    sw[i] = (j == 0 && lane == 0) ? hid[i] : r;
-                }
-#pragma unroll
-                for (int i = 0; i < EPV; ++i) sw[H + i] = id[j][i];
-            }
-#pragma unroll
-            for (int i = 0; i < EPV; ++i) {
-                const float g = vget<T>(gv[j], i);
-                float d = g;
-                if constexpr (SILU) {
-                    // q = -log2(e) * pre, from pre-scaled weights and bias
-                    float q = bq;
-#pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if constexpr (SEQ) {
-                            if (sw[i + k] == sw[H + i]) q = __builtin_fmaf(wq[k], win[i + k], q);
-                        } else {
-                            q = __builtin_fmaf(wq[k], win[i + k], q);
-                        }
-                    }
-                    d = silu_bwd_q(g, q);
-                }
-                if (!FULL && t >= L) d = 0.0f;
-                if constexpr (SEQ) {
-                    if (sw[H + i] < 0) d = 0.0f;
-                }
-                dp[j][i] = d;
-                pb += d;
-#pragma unroll
-                for (int k = 0; k < W; ++k) {
-                    if constexpr (SEQ) {
-                        if (sw[i + k] == sw[H + i]) pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
-                    } else {
-                        pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
-                    }
-                }
-            }
-        }
-
-        // ---- dpre of the first H positions of the next segment (used by lane 63;
-        //      zero when this segment ends the row) ----
-        float dn[H];
-#pragma unroll
-        for (int i = 0; i < H; ++i) dn[i] = 0.0f;
-        if (tn < L) {
-            float xw[2 * H];
-            int32_t iw[2 * H];
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                xw[i] = vget<T>(v[VPT - 1], EPV - H + i);
-                xw[H + i] = vget<T>(xn, i);
-                if constexpr (SEQ) {
-                    iw[i] = id[VPT - 1][EPV - H + i];
-                    iw[H + i] = nid[i];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const float g = vget<T>(gn, i);
-                float d = g;
-                if constexpr (SILU) {
-                    float q = bq;
-#pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if constexpr (SEQ) {
-                            if (iw[i + k] == iw[H + i]) q = __builtin_fmaf(wq[k], xw[i + k], q);
-                        } else {
-                            q = __builtin_fmaf(wq[k], xw[i + k], q);
-                        }
-                    }
-                    d = silu_bwd_q(g, q);
-                }
-                if (tn + i >= L) d = 0.0f;
-                if constexpr (SEQ) {
-                    if (iw[H + i] < 0) d = 0.0f;
-                }
-                dn[i] = d;
-            }
-        }
-
-        // ---- dx ----
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int32_t t = t0 + (j * 64 + lane) * EPV;
-            float de[EPV + H];
-            int32_t ie[EPV + H];
-#pragma unroll
-            for (int i = 0; i < EPV; ++i) {
-                de[i] = dp[j][i];
-                if constexpr (SEQ) ie[i] = id[j][i];
-            }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                const float send = (lane == 0) ? (j + 1 < VPT ? dp[j + 1 < VPT ? j + 1 : 0][i] : 0.0f) : dp[j][i];
-                const float r = lane_get(send, next_lane);
-                de[EPV + i] = (lane == 63 && j == VPT - 1) ? dn[i] : r;
-                if constexpr (SEQ) {
-                    const int32_t s = (lane == 0) ? (j + 1 < VPT ? id[j + 1 < VPT ? j + 1 : 0][i] : -1) : id[j][i];
-                    const int32_t ri = lane_get(s, next_lane);
-                    ie[EPV + i] = (lane == 63 && j == VPT - 1) ? nid[i] : ri;
-                }
-            }
-            float o[EPV];
-#pragma unroll
-            for (int i = 0; i < EPV; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k < W; ++k) {
-                    if constexpr (SEQ) {
-                        if (ie[i + k] == ie[i]) acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
-                    } else {
-                        acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
-                    }
-                }
-                o[i] = acc;
-            }
-            // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
-            // here, so the W-1 tail positions are the end of the last vector.
-            // A wave-uniform branch skips it for every segment without the row
-            // end (as a lane-masked block it was issued, empty, by all of them).
-            if (dfin_row) {
-                const bool last = t + EPV == L;
-#pragma unroll
-                for (int i = EPV - H; i < EPV; ++i) {
-                    const float v = round_to<T>(o[i]) + dfin[H - EPV + i];
-                    o[i] = last ? v : o[i];
-                }
-            }
-            if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
-        }
-
-        // ---- dinitial_states (bwd_full_cpu/kernel.mojo:210-219) ----
-        if (p.dinitial_states != nullptr && t0 == 0 && lane == 0) {
-            T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
-                    c * p.dinitial_states_stride[1];
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], dp[0][i - k], acc);
-                st(di, i * p.dinitial_states_stride[2], acc);
-            }
-        }
-    }
-}
-
-template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
-__device__ __forceinline__ void bwd_rows_segment(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0, const float* w, const float* wq, float bq, float* pw,
-                                                 float& pb) {
-    RowTile<VPT> r;
-    bwd_rows_load<T, VPT, FULL>(p, lane, b, c, t0, r);
-    bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
-}
-
-// One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
-// segment) with row = b * dim + c, in memory order like the forward, so
-// consecutive wavefronts stream consecutive rows. The wavefront sums its
-// weight/bias-gradient partials with DPP adds, and lanes 0..W add them to
-// the fp32 accumulators (one atomic instruction) or write the item's partial
-// record. All index arithmetic is 32-bit (the launcher checks the ranges).
-template <typename T, int W, int VPT, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(64 * kRowsWPB) bwd_rows_vec(const BwdArgs a) {
-    constexpr int SEG = 64 * VPT * elems16<T>::value;
-    const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const uint32_t item = uniform32(blockIdx.x * (uint32_t)kRowsWPB + (threadIdx.x >> 6));
-    if (item >= (uint32_t)a.n_items) return;
-    const uint32_t nseg = (uint32_t)a.nseg;
-    const uint32_t row = item / nseg;
-    const int32_t t0 = (int32_t)((item - row * nseg) * SEG);
-    const uint32_t dim = (uint32_t)p.dim;
-    const uint32_t b = row / dim;
-    const uint32_t c = row - b * dim;
-
-    float w[W];
-    const T* __restrict__ wr = static_cast<const T*>(p.weight) + (int64_t)c * p.weight_stride[0];
-#pragma unroll
-    for (int k = 0; k < W; ++k) w[k] = ld_uniform(wr + k * p.weight_stride[1]);
-    const float bias = p.bias ? ld_uniform(static_cast<const T*>(p.bias) + (int64_t)c * p.bias_stride) : 0.0f;
-    float wq[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) wq[k] = -kLog2e * w[k];
-    const float bq = -kLog2e * bias;
-
-    float pw[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
-    float pb = 0.0f;
-    if (t0 + SEG <= (int32_t)p.seqlen)
-        bwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0, w, wq, bq, pw, pb);
-    else
-        bwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0, w, wq, bq, pw, pb);
-
-    // ---- weight / bias gradient: wavefront sum, then lanes 0..W add ----
-    float mine = wave_sum(pb);
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-        const float s = wave_sum(pw[k]);
-        if (lane == k) mine = s;
-    }
-    if (a.part != nullptr) {  // record (W taps, bias) of this item
-        if (lane <= W) a.part[(int64_t)item * (W + 1) + lane] = mine;
-    } else if (lane < W) {
-        unsafeAtomicAdd(p.dweight_acc + (int64_t)c * p.dweight_acc_stride[0] + lane * p.dweight_acc_stride[1], mine);
-    } else if (lane == W && p.dbias_acc != nullptr) {
-        unsafeAtomicAdd(p.dbias_acc + (int64_t)c * p.dbias_acc_stride, mine);
-    }
-}
-
-// One channel c of batch b over steps [t0, t1), any strides: writes dx (and
-// dinitial_states when t0 == 0) and returns the chunk's weight/bias-gradient
-// partials in pw / pb. Windows of the previous W-1 positions are rolled in
-// registers; the step loop is not unrolled, so the register footprint is
-// small.
-template <typename T, int W, bool SILU>
-__device__ __forceinline__ void bwd_chunk(const cc1d_bwd_params& p, int64_t b, int64_t c, int64_t t0, int64_t t1,
-                                          float* pw, float& pb) {
-    constexpr int H = W - 1;
-    const int64_t L = p.seqlen;
-    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
-    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
-    T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
-    const int32_t* sr = p.seq_idx ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
-    const T* ir = p.initial_states ? static_cast<const T*>(p.initial_states) + b * p.initial_states_stride[0] +
-                                         c * p.initial_states_stride[1]
-                                   : nullptr;
-
-    float w[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k)
-        w[k] = ld(static_cast<const T*>(p.weight), c * p.weight_stride[0] + k * p.weight_stride[1]);
-    const float bias = p.bias ? ld(static_cast<const T*>(p.bias), c * p.bias_stride) : 0.0f;
-
-    // Windows over positions s-H..s: x values, seq ids, dpre values.
-    float xw[W], dw[W];
-    int32_t iw[W];
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-        const int64_t s = t0 - H + i;
-        if (s >= 0) xw[i] = ld(xr, s * p.x_stride[2]);
-        else xw[i] = ir ? ld(ir, (s + H) * p.initial_states_stride[2]) : 0.0f;
-        iw[i] = (sr != nullptr && s >= 0) ? sr[s * p.seq_idx_stride[1]] : -1;
-        dw[i] = 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < W; ++k) pw[k] = 0.0f;
-    pb = 0.0f;
-    float dfirst[H];
-#pragma unroll
-    for (int i = 0; i < H; ++i) dfirst[i] = 0.0f;
-
-    const int64_t m = (H < L) ? H : L;  // dfinal tail length
-    for (int64_t s = t0; s < t1 + H; ++s) {
-        const bool in = s < L;
-        xw[H] = in ? ld(xr, s * p.x_stride[2]) : 0.0f;
-        iw[H] = (in && sr != nullptr) ? sr[s * p.seq_idx_stride[1]] : -1;
-        float d = 0.0f;
-        if (in) {
-            const float g = ld(gr, s * p.dout_stride[2]);
-            d = g;
-            if (SILU) {
-                float pre = bias;
-#pragma unroll
-                for (int k = 0; k < W; ++k)
-                    if (sr == nullptr || iw[k] == iw[H]) pre = __builtin_fmaf(w[k], xw[k], pre);
-                d = g * silu_grad(pre);
-            }
-            if (sr != nullptr && iw[H] < 0) d = 0.0f;
-        }
-        dw[H] = d;
-        if (s < t1) {
-            pb += d;
-#pragma unroll
-            for (int k = 0; k < W; ++k)
-                if (sr == nullptr || iw[k] == iw[H]) pw[k] = __builtin_fmaf(d, xw[k], pw[k]);
-#pragma unroll
-            for (int i = 0; i < H; ++i)
-                if (s == i) dfirst[i] = d;
-        }
-        const int64_t q = s - H;
-        if (q >= t0) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < W; ++k)
-                if (sr == nullptr || iw[k] == iw[0]) acc = __builtin_fmaf(w[W - 1 - k], dw[k], acc);
-            if (p.dfinal_states != nullptr && q >= L - m)
-                acc = round_to<T>(acc) + ld(static_cast<const T*>(p.dfinal_states),
-                                            b * p.dfinal_states_stride[0] + c * p.dfinal_states_stride[1] +
-                                                (q - L + H) * p.dfinal_states_stride[2]);
-            st(dxr, q * p.dx_stride[2], acc);
-        }
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-            xw[i] = xw[i + 1];
-            iw[i] = iw[i + 1];
-            dw[i] = dw[i + 1];
-        }
-    }
-    if (p.dinitial_states != nullptr && t0 == 0) {
-        T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] + c * p.dinitial_states_stride[1];
-#pragma unroll
-        for (int i = 0; i < H; ++i) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], dfirst[i - k], acc);
-            st(di, i * p.dinitial_states_stride[2], acc);
-        }
-    }
-}
-
-// ---- channel-last (unit channel stride) backward: a walk along time ------
-//
-// A lane owns CPL adjacent channels (4 bytes) and a wavefront the 64 * CPL
-// channels of one run of R time steps [t0, t0 + R). The wavefront walks its
-// run in chunks of G steps, one 256-byte row of x and of dout per load
-// instruction, the next chunk's loads in flight while the current chunk is
-// computed. x and dpre of the last H = W - 1 positions slide in registers;
-// dx of position s is emitted once dpre[s + H] is known, so a run computes
-// dpre for [t0, t0 + R + H) (a tail of H steps, the next run's first) and
-// emits dx for [t0, t0 + R). Loads are unconditional at positions clamped
-// into [0, L); a chunk whose window lies inside the sequence with one
-// seq_idx id (>= 0) takes the ungated arithmetic, any other chunk the same
-// steps with every condition applied (all of them wave-uniform: one time
-// step per instruction row, the ids in scalar registers). Index arithmetic
-// is 32-bit inside a batch (the launcher checks the ranges).
-//
-// Launch shape (C3, 8192 x 4096 bf16): chunks of 4 steps, runs of 128, 8
-// runs per block -- 2048 wavefronts, two per SIMD. Measured against it
-// (same box, us for seq_idx / initial_states): tiles of 16 steps loaded at
-// once, 4 per block, 46.3 / 45.0 (the previous kernel); runs of 64 or 96
-// steps 48-49; runs of 192 52-57; chunks of 8 steps 46-48; 4 runs per block
-// 44.0 / 42.0; 8 runs per block 42.1 / 41.0. A copy with the same access
-// pattern and no arithmetic takes 36.8 us.
-
-// The weights and bias of a lane's channels, kept raw: they are read before
-// the walk and converted where they are used, so no conversion waits for
-// them (memory counters retire in order) ahead of the first chunk's loads.
-// Without a bias the bias read goes to x's first element (an unconditional
-// load, so no branch waits on it) and bias() returns zero.
-template <typename T, int W, int CPL> struct ClWeights {
-    T w[W][CPL], b[CPL];
-    bool has_bias;
-    __device__ __forceinline__ void load(const cc1d_bwd_params& p, int32_t c0, bool active) {
-        const T* __restrict__ wp = static_cast<const T*>(p.weight);
-        has_bias = p.bias != nullptr;
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-            const int64_t c = active ? c0 + e : 0;
-#pragma unroll
-            for (int k = 0; k < W; ++k) w[k][e] = wp[c * p.weight_stride[0] + k * p.weight_stride[1]];
-            const T* bsrc = has_bias ? static_cast<const T*>(p.bias) + c * p.bias_stride : static_cast<const T*>(p.x);
-            b[e] = *bsrc;
-        }
-    }
-    __device__ __forceinline__ float bias(int e) const { return has_bias ? to_f32(b[e]) : 0.0f; }
-};
-
-// G rows of x and dout from position c0 on, raw; ids[i]: seq_idx at position
-// c0 - H + i (clamped into [0, L)), read through the scalar cache (NI = G + H
-// with seq_idx, else 1 unused).
-template <typename T, int CPL, int G, int NI> struct ClChunk {
-    Lanes<T, CPL> x[G], g[G];
-    int32_t ids[NI];
-};
-
-// Sliding state of a walk: x and dpre at the H positions before the current
-// one (x zero before the sequence or initial_states there, dpre zero before
-// the run), and the weight/bias-gradient partial sums.
-template <int W, int CPL> struct ClWalk {
-    float xw[W - 1][CPL], dw[W - 1][CPL];
-    float pw[W][CPL], pb[CPL];
-    // Ends a step's partial-sum updates where they are written: otherwise the
-    // compiler sinks each running sum's fma towards its next use (the next
-    // step's), until a chunk's updates all sit at its end and every step's
-    // dpre and x stay live until then.
-    __device__ __forceinline__ void pin_sums() {
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-            for (int k = 0; k < W; ++k) asm volatile("" : "+v"(pw[k][e]));
-            asm volatile("" : "+v"(pb[e]));
-        }
-    }
-};
-
-// One dword of a row at byte offset off from the wavefront-uniform base
-// (offsets below 2^32: the launcher checks the ranges). A 64-bit uniform base
-// plus a 32-bit per-lane offset is the scalar-base form of the global
-// access (global_load_dword v, v_off, s[base]): one 32-bit add per access.
-// Non-temporal: a walk reads each row once (the few rows a neighbouring run
-// reads again are its H-row prime and tail); at C3 the backward took 37.3 /
-// 38.5 us with non-temporal row loads against 40.5 / 41.3 us with cached ones.
-template <typename T, int CPL> __device__ __forceinline__ Lanes<T, CPL> row_load(const T* base, uint32_t off) {
-    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
-    Lanes<T, CPL> v;
-    v.d[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(base) + off));
-    return v;
-}
-template <typename T, int CPL> __device__ __forceinline__ void row_store_nt(T* base, uint32_t off, const Lanes<T, CPL>& v) {
-    static_assert(Lanes<T, CPL>::ND == 1, "one dword per lane");
-    __builtin_nontemporal_store(v.d[0], reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(base) + off));
-}
-
-// Kernel: the WPB wavefronts of a block take WPB consecutive runs of the same
-// channels; their weight/bias-gradient partials are summed through LDS and
-// the block adds the sums with fp32 atomics on consecutive addresses (or
-// writes them as its record). Block order: channel group fastest, then run
-// group, then batch.
-template <typename T, int W, int G, int R, int WPB, bool SILU, bool SEQ>
-__global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
-    constexpr int CPL = 4 / (int)sizeof(T);
-    constexpr int H = W - 1;
-    constexpr int NC = 64 * CPL;  // channels per wavefront
-    constexpr int NCH = R / G;    // chunks per run
-    static_assert(R == G || (R % (2 * G) == 0 && R >= 2 * G), "one chunk, or chunks in pairs");
-    static_assert(G >= H, "the first chunk covers the H steps whose dx belongs to the previous run");
-    using Chunk = ClChunk<T, CPL, G, SEQ ? G + H : 1>;
-    __shared__ float red[WPB][NC * (W + 1)];
-    const cc1d_bwd_params& p = a.p;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    // (the divisions run on the vector unit; uniform32 brings the results
-    // back to scalar registers, so every pointer derived from them is scalar)
-    const uint32_t ngroups = (uint32_t)a.groups, ntgroups = (uint32_t)a.nseg;
-    const uint32_t grp = uniform32(blockIdx.x % ngroups);
-    const uint32_t rest = uniform32(blockIdx.x / ngroups);
-    const uint32_t tg = uniform32(rest % ntgroups);
-    const uint32_t b = uniform32(rest / ntgroups);
-    const int32_t L = (int32_t)p.seqlen;
-    const int32_t t0 = (int32_t)uniform32((tg * WPB + wave) * R);
-    const int32_t cw0 = (int32_t)(grp * NC);
-    const int32_t c0 = cw0 + lane * CPL;
-    const bool active = c0 < (int32_t)p.dim;
-
-    ClWalk<W, CPL> s;
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-        s.pb[e] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < W; ++k) s.pw[k][e] = 0.0f;
-    }
-    if (t0 < L) {  // runs past the end only join the block reduction
-        const int32_t xs2 = (int32_t)p.x_stride[2], gs2 = (int32_t)p.dout_stride[2];
-        const int32_t ds2 = (int32_t)p.dx_stride[2];
-        // lanes past the last channel read channel 0 of the group's rows (in
-        // bounds); they store nothing and their partials are dropped
-        const int32_t lo = active ? lane * CPL : 0;
-        const uint32_t lob = (uint32_t)lo * (uint32_t)sizeof(T);  // the lane's byte offset in a row
-        const T* __restrict__ xb = static_cast<const T*>(p.x) + b * p.x_stride[0] + cw0;
-        const T* __restrict__ gb = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + cw0;
-        T* __restrict__ dxb = static_cast<T*>(p.dx) + b * p.dx_stride[0] + cw0;
-        const int32_t* __restrict__ sr = SEQ ? p.seq_idx + b * p.seq_idx_stride[0] : nullptr;
-        const int32_t ss1 = SEQ ? (int32_t)p.seq_idx_stride[1] : 0;
-        auto clampL = [&](int32_t t) { return t < 0 ? 0 : (t < L ? t : L - 1); };
-
-        // loads of the rows of chunk c (NR of them) and of its id window
-        auto load = [&](int32_t cs, Chunk& ch, auto nr) {
-            constexpr int NR = decltype(nr)::value;
-#pragma unroll
-            for (int j = 0; j < NR; ++j) {
-                const int32_t t = clampL(cs + j);
-                ch.x[j] = row_load<T, CPL>(xb, (uint32_t)(t * xs2) * (uint32_t)sizeof(T) + lob);
-                ch.g[j] = row_load<T, CPL>(gb, (uint32_t)(t * gs2) * (uint32_t)sizeof(T) + lob);
-            }
-            if constexpr (SEQ) {
-                constexpr int NI = G + H;
-                if (ss1 == 1 && cs >= H && cs - H + NI <= L) {
-                    // the window's ids are consecutive and in range: one scalar load
-                    const __attribute__((address_space(4))) int32_t* q =
-                        (const __attribute__((address_space(4))) int32_t*)reinterpret_cast<uintptr_t>(sr + (cs - H));
-#pragma unroll
-                    for (int i = 0; i < NI; ++i) ch.ids[i] = q[i];
-                } else {
-#pragma unroll
-                    for (int i = 0; i < NI; ++i) ch.ids[i] = ld_uniform(sr + clampL(cs - H + i) * ss1);
-                }
-            }
-        };
-
-        // x rows t0-H .. t0-1 (zero before the sequence, or initial_states)
-        Lanes<T, CPL> prime[H];
-        const bool prime_rows = t0 >= H;
-        if (prime_rows) {
-#pragma unroll
-            for (int k = 0; k < H; ++k)
-                prime[k] = row_load<T, CPL>(xb, (uint32_t)((t0 - H + k) * xs2) * (uint32_t)sizeof(T) + lob);
-        }
-        ClWeights<T, W, CPL> wt;
-        wt.load(p, c0, active);
-        Chunk A, B;
-        load(t0, A, std::integral_constant<int, G>{});
-
-        // w for dx; wq, bq (scaled by -log2(e)) give the SiLU argument q = -log2(e) * pre
-        // directly, as the exponent silu_bwd_q takes
-        float w[W][CPL], wq[W][CPL], bq[CPL];
-#pragma unroll
-        for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-            for (int k = 0; k < W; ++k) {
-                w[k][e] = to_f32(wt.w[k][e]);
-                wq[k][e] = -kLog2e * w[k][e];
-            }
-            bq[e] = -kLog2e * wt.bias(e);
-        }
-#pragma unroll
-        for (int k = 0; k < H; ++k) {
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                s.xw[k][e] = prime_rows ? prime[k].get(e) : 0.0f;
-                s.dw[k][e] = 0.0f;
-            }
-        }
-        if (!prime_rows && p.initial_states != nullptr && active) {  // t0 == 0
-            const int32_t cl = opaque(c0);
-#pragma unroll
-            for (int k = 0; k < H; ++k)
-#pragma unroll
-                for (int e = 0; e < CPL; ++e)
-                    s.xw[k][e] = ld(static_cast<const T*>(p.initial_states),
-                                    b * p.initial_states_stride[0] + (cl + e) * p.initial_states_stride[1] +
-                                        k * p.initial_states_stride[2]);
-        }
-        const int32_t m = H < L ? H : L;  // dfinal tail length
-
-        // shift the windows by one position: x and dpre of the current step enter
-        auto slide = [&](const float* xc, const float* dn) {
-#pragma unroll
-            for (int k = 0; k + 1 < H; ++k)
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    s.xw[k][e] = s.xw[k + 1][e];
-                    s.dw[k][e] = s.dw[k + 1][e];
-                }
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                s.xw[H - 1][e] = xc[e];
-                s.dw[H - 1][e] = dn[e];
-            }
-        };
-        auto store_dx = [&](int32_t pos, const float* o) {
-            Lanes<T, CPL> ov;
-            ov.set(o);
-            row_store_nt<T, CPL>(dxb, (uint32_t)(pos * ds2) * (uint32_t)sizeof(T) + lob, ov);
-        };
-
-        // NS steps of chunk ch at cs, ungated (the chunk's window [cs-H, cs+NS+H)
-        // lies in [0, L) with one id); ACC: the steps are the run's own;
-        // HEAD: the run's first chunk (dx before the run belongs to the
-        // previous one)
-        auto steps_clean = [&](const Chunk& ch, int32_t cs, auto ns, auto accc, auto headc) {
-            constexpr int NS = decltype(ns)::value;
-            constexpr bool ACC = decltype(accc)::value;
-            constexpr bool HEAD = decltype(headc)::value;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                float xc[CPL], dn[CPL], o[CPL];
-                const Lanes<T, CPL> xl = ch.x[j], gl = ch.g[j];
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    xc[e] = xl.get(e);
-                    const float gval = gl.get(e);
-                    float d = gval;
-                    if constexpr (SILU) {
-                        float q = bq[e];
-#pragma unroll
-                        for (int k = 0; k < H; ++k) q = __builtin_fmaf(wq[k][e], s.xw[k][e], q);
-                        q = __builtin_fmaf(wq[H][e], xc[e], q);
-                        d = silu_bwd_q(gval, q);
-                    }
-                    dn[e] = d;
-                    if constexpr (ACC) {
-                        s.pb[e] += d;
-#pragma unroll
-                        for (int k = 0; k < H; ++k) s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
-                        s.pw[H][e] = __builtin_fmaf(d, xc[e], s.pw[H][e]);
-                    }
-                    // dx at position cs + j - H: dpre there .. here, taps w[H] .. w[0]
-                    float acc = 0.0f;
-#pragma unroll
-                    for (int k = 0; k < H; ++k) acc = __builtin_fmaf(w[H - k][e], s.dw[k][e], acc);
-                    o[e] = __builtin_fmaf(w[0][e], d, acc);
-                }
-                if (active && (j >= H || !HEAD)) store_dx(cs + j - H, o);
-                slide(xc, dn);
-                if constexpr (ACC) s.pin_sums();
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        };
-
-        // the same steps with every condition: positions past the end,
-        // seq_idx gates, dfinal_states, dinitial_states (chunk 0 of run 0)
-        auto steps_gated = [&](const Chunk& ch, int32_t cs, auto ns, auto accc) {
-            constexpr int NS = decltype(ns)::value;
-            constexpr bool ACC = decltype(accc)::value;
-#pragma unroll
-            for (int j = 0; j < NS; ++j) {
-                const int32_t pos = cs + j;
-                const bool in = pos < L;
-                int32_t idk[H], idp = 0;  // ids of the window positions and of pos
-                if constexpr (SEQ) {
-#pragma unroll
-                    for (int k = 0; k < H; ++k) idk[k] = ch.ids[j + k];
-                    idp = ch.ids[j + H];
-                } else {
-#pragma unroll
-                    for (int k = 0; k < H; ++k) idk[k] = 0;
-                }
-                const bool dead = !in || idp < 0;
-                float xc[CPL], dn[CPL];
-                const Lanes<T, CPL> xl = ch.x[j], gl = ch.g[j];
-#pragma unroll
-                for (int e = 0; e < CPL; ++e) {
-                    xc[e] = in ? xl.get(e) : 0.0f;
-                    const float gval = gl.get(e);
-                    float d = gval;
-                    if constexpr (SILU) {
-                        float q = bq[e];
-#pragma unroll
-                        for (int k = 0; k < H; ++k)
-                            if (idk[k] == idp) q = __builtin_fmaf(wq[k][e], s.xw[k][e], q);
-                        q = __builtin_fmaf(wq[H][e], xc[e], q);
-                        d = silu_bwd_q(gval, q);
-                    }
-                    if (dead) d = 0.0f;
-                    dn[e] = d;
-                    if constexpr (ACC) {
-                        s.pb[e] += d;
-#pragma unroll
-                        for (int k = 0; k < H; ++k)
-                            if (idk[k] == idp) s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
-                        s.pw[H][e] = __builtin_fmaf(d, xc[e], s.pw[H][e]);
-                    }
-                }
-                // dx at position sp = pos - H: tap k kept when id(sp + k) == id(sp)
-                const int32_t sp = pos - H;
-                if (sp >= t0 && sp < L && active) {
-                    float o[CPL];
-#pragma unroll
-                    for (int e = 0; e < CPL; ++e) {
-                        float acc = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < H; ++k)
-                            if (idk[k] == idk[0]) acc = __builtin_fmaf(w[H - k][e], s.dw[k][e], acc);
-                        if (idp == idk[0]) acc = __builtin_fmaf(w[0][e], dn[e], acc);
-                        o[e] = acc;
-                    }
-                    if (p.dfinal_states != nullptr && sp >= L - m) {
-                        const int32_t cl = opaque(c0);
-#pragma unroll
-                        for (int e = 0; e < CPL; ++e)
-                            o[e] = round_to<T>(o[e]) + ld(static_cast<const T*>(p.dfinal_states),
-                                                          b * p.dfinal_states_stride[0] +
-                                                              (cl + e) * p.dfinal_states_stride[1] +
-                                                              (sp - L + H) * p.dfinal_states_stride[2]);
-                    }
-                    store_dx(sp, o);
-                }
-                slide(xc, dn);
-                if constexpr (ACC) s.pin_sums();
-                // dinitial_states (bwd_full_cpu/kernel.mojo:210-219): once the
-                // window holds dpre[0 .. H-1] (position H-1 is step H-1 of the
-                // chunk at 0, as chunks start at multiples of G >= H)
-                if (j == H - 1 && cs == 0 && p.dinitial_states != nullptr && active) {
-                    const int32_t cl = opaque(c0);
-#pragma unroll
-                    for (int e = 0; e < CPL; ++e) {
-                        T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
-                                (cl + e) * p.dinitial_states_stride[1];
-#pragma unroll
-                        for (int i = 0; i < H; ++i) {
-                            float acc = 0.0f;
-#pragma unroll
-                            for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k][e], s.dw[i - k][e], acc);
-                            st(di, i * p.dinitial_states_stride[2], acc);
-                        }
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        };
-
-        // a chunk is clean when its window [cs-H, cs+NS+H) lies inside the
-        // sequence (the last H positions: dfinal_states reach back that far)
-        // and, with seq_idx, carries one id >= 0
-        auto steps = [&](const Chunk& ch, int32_t cs, auto ns, auto accc, auto headc) {
-            constexpr int NS = decltype(ns)::value;
-            bool clean = cs >= H && cs + NS + H <= L;
-            if constexpr (SEQ) {
-                const int32_t id0 = ch.ids[0];
-                bool same = id0 >= 0;
-#pragma unroll
-                for (int i = 1; i < NS + H; ++i) same = same && ch.ids[i] == id0;
-                clean = clean && same;
-            }
-            if (clean) steps_clean(ch, cs, ns, accc, headc);
-            else steps_gated(ch, cs, ns, accc);
-        };
-
-        constexpr std::integral_constant<int, G> kG{};
-        constexpr std::integral_constant<int, H> kH{};
-        constexpr std::true_type kAcc{};
-        constexpr std::false_type kNoAcc{};
-        constexpr std::true_type kHead{};
-        constexpr std::false_type kBody{};
-        if constexpr (NCH == 1) {
-            // the whole run at once: its rows and the tail's are all in flight
-            load(t0 + R, B, kH);  // the tail: the next run's first H rows
-            steps(A, t0, kG, kAcc, kHead);
-            steps(B, t0 + R, kH, kNoAcc, kBody);
-        } else {
-            // chunk 0 in A, chunk 1 in B; then chunks in pairs, each buffer
-            // refilled as soon as it has been consumed; the tail last
-            load(t0 + G, B, kG);
-            steps(A, t0, kG, kAcc, kHead);
-#pragma unroll 1
-            for (int c = 1; c + 1 < NCH; c += 2) {
-                const int32_t cb = t0 + c * G;
-                load(cb + G, A, kG);
-                steps(B, cb, kG, kAcc, kBody);
-                load(cb + 2 * G, B, kG);
-                steps(A, cb + G, kG, kAcc, kBody);
-            }
-            load(t0 + R, A, kH);  // the tail: the next run's first H rows
-            steps(B, t0 + R - G, kG, kAcc, kBody);
-            steps(A, t0 + R, kH, kNoAcc, kBody);
-        }
-        if (!active) {
-#pragma unroll
-            for (int e = 0; e < CPL; ++e) {
-                s.pb[e] = 0.0f;
-#pragma unroll
-                for (int k = 0; k < W; ++k) s.pw[k][e] = 0.0f;
-            }
-        }
-    }
-
-    // ---- weight / bias gradient: sum the block's runs in LDS, then
-    //      consecutive fp32 atomics (or the block's record) ----
-    float* rr = red[wave];
-#pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-#pragma unroll
-        for (int k = 0; k < W; ++k) rr[(lane * CPL + e) * W + k] = s.pw[k][e];
-        rr[NC * W + lane * CPL + e] = s.pb[e];
-    }
-    __syncthreads();
-    constexpr int NE = NC * (W + 1);
-    for (int idx = threadIdx.x; idx < NE; idx += 64 * WPB) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int q = 0; q < WPB; ++q) sum += red[q][idx];
-        if (a.part != nullptr) {  // the block's record: NC channels x W taps, then NC bias sums
-            a.part[(int64_t)blockIdx.x * NE + idx] = sum;
-        } else if (idx < NC * W) {
-            const int32_t c = cw0 + idx / W;
-            if (c < (int32_t)p.dim)
-                unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + (idx % W) * p.dweight_acc_stride[1], sum);
-        } else if (p.dbias_acc != nullptr) {
-            const int32_t c = cw0 + (idx - NC * W);
-            if (c < (int32_t)p.dim) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, sum);
-        }
-    }
-}
-
-template <typename T, int W, bool SILU>
-__global__ void __launch_bounds__(256) bwd_generic(const BwdArgs a) {
-    constexpr int H = W - 1;
-    const cc1d_bwd_params& p = a.p;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.n_items) return;
-    const int64_t c = idx % p.dim;
-    const int64_t rest = idx / p.dim;
-    const int64_t ch = rest % a.nseg;
-    const int64_t b = rest / a.nseg;
-    const int64_t t0 = ch * a.chunk;
-    const int64_t t1 = (t0 + a.chunk < p.seqlen) ? t0 + a.chunk : p.seqlen;
-    float pw[W], pb;
-    bwd_chunk<T, W, SILU>(p, b, c, t0, t1, pw, pb);
-    (void)H;
-    if (a.part != nullptr) {  // record (W taps, bias) of this thread's chunk
-#pragma unroll
-        for (int k = 0; k < W; ++k) a.part[idx * (W + 1) + k] = pw[k];
-        a.part[idx * (W + 1) + W] = pb;
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < W; ++k)
-        unsafeAtomicAdd(p.dweight_acc + c * p.dweight_acc_stride[0] + k * p.dweight_acc_stride[1], pw[k]);
-    if (p.dbias_acc != nullptr) unsafeAtomicAdd(p.dbias_acc + c * p.dbias_acc_stride, pb);
-}
-
-namespace {
-
-template <typename T>
-bool rows_vec_ok(const cc1d_bwd_params& p) {
-    constexpr int64_t EPV = elems16<T>::value;
-    if (p.width - 1 > EPV) return false;
-    if (p.x_stride[2] != 1 || p.dout_stride[2] != 1 || p.dx_stride[2] != 1) return false;
-    if (p.seqlen % EPV != 0) return false;
-    if (!aligned16(p.x) || !aligned16(p.dout) || !aligned16(p.dx)) return false;
-    if (p.x_stride[0] % EPV || p.x_stride[1] % EPV || p.dout_stride[0] % EPV || p.dout_stride[1] % EPV ||
-        p.dx_stride[0] % EPV || p.dx_stride[1] % EPV)
-        return false;
-    if (p.seq_idx != nullptr &&
-        (p.seq_idx_stride[1] != 1 || p.seq_idx_stride[0] % 4 != 0 || !aligned16(p.seq_idx)))
-        return false;
-    // 32-bit index arithmetic: positions and items (one block each) must fit
-    if (p.seqlen + 64 * 4 * EPV >= ((int64_t)1 << 31)) return false;
-    if (p.batch * p.dim * ceil_div(p.seqlen, 64 * EPV) >= ((int64_t)1 << 31)) return false;
-    return true;
-}
-
-// channel-last tiles: unit channel stride, CPL | dim, rows aligned to the
-// CPL-channel lane vector, 32-bit positions inside a batch
-template <typename T, int CPL>
-bool cl_ok(const cc1d_bwd_params& p) {
-    constexpr int64_t NB = CPL * (int64_t)sizeof(T);
-    if (p.x_stride[1] != 1 || p.dout_stride[1] != 1 || p.dx_stride[1] != 1) return false;
-    if (p.dim % CPL != 0) return false;
-    if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.dout) |
-         reinterpret_cast<uintptr_t>(p.dx)) % NB)
-        return false;
-    if (p.x_stride[0] % CPL || p.x_stride[2] % CPL || p.dout_stride[0] % CPL || p.dout_stride[2] % CPL ||
-        p.dx_stride[0] % CPL || p.dx_stride[2] % CPL)
-        return false;
-    const int64_t span = p.seqlen + kClWPB * kClR + 16;  // past the furthest run start
-    const int64_t lim = (int64_t)1 << 31;
-    if (p.dim >= lim || span * p.x_stride[2] >= lim || span * p.dout_stride[2] >= lim || span * p.dx_stride[2] >= lim)
-        return false;
-    if (p.seq_idx != nullptr && span * p.seq_idx_stride[1] >= lim) return false;
-    if (p.batch * ceil_div(p.dim / CPL, 64) * ceil_div(p.seqlen, kClR * kClWPB) >= lim) return false;
-    return true;
-}
-
-
-// ---- launch planning ----------------------------------------------------
-
-enum BwdKind { kBwdRows = 0, kBwdCl = 1, kBwdGeneric = 2 };
-
-// Kernel choice and launch geometry for one call; shared by the launch, the
-// workspace size and the partial-sum reduction.
-struct BwdPlan {
-    int kind;
-    int vpt;           // rows: 16-byte vectors per lane
-    int cpl;           // cl: channels per lane
-    BwdArgs a;
-    int64_t blocks;
-    int64_t records;   // partial-sum records (rows / generic: items; cl: blocks)
-    int64_t rec_floats;
-};
-
-template <typename T, int W>
-BwdPlan plan_bwd(const cc1d_bwd_params& p) {
-    constexpr int64_t EPV = elems16<T>::value;
-    BwdPlan pl;
-    pl.a.p = p;
-    pl.a.part = nullptr;
-    pl.a.chunk = 0;
-    pl.a.groups = 0;
-    pl.vpt = 0;
-    pl.cpl = 0;
-    pl.rec_floats = W + 1;
-    if (W - 1 <= EPV && rows_vec_ok<T>(p)) {
-        const int64_t nvec = p.seqlen / EPV;
-        const int64_t per = ceil_div(nvec, 64);
-        pl.kind = kBwdRows;
-        pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
-        pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
-        pl.a.n_items = p.batch * p.dim * pl.a.nseg;
-        pl.blocks = ceil_div(pl.a.n_items, (int64_t)kRowsWPB);
-        pl.records = pl.a.n_items;
-        return pl;
-    }
-    constexpr int CPL = 4 / (int)sizeof(T);
-    if (cl_ok<T, CPL>(p)) {
-        pl.kind = kBwdCl;
-        pl.cpl = CPL;
-        pl.a.groups = ceil_div(p.dim / CPL, 64);
-        pl.a.chunk = kClR;
-        pl.a.nseg = ceil_div(p.seqlen, kClR * kClWPB);  // run groups per row
-        pl.a.n_items = 0;
-        pl.blocks = p.batch * pl.a.groups * pl.a.nseg;
-        pl.records = pl.blocks;
-        pl.rec_floats = 64 * CPL * (W + 1);
-        return pl;
-    }
-    pl.kind = kBwdGeneric;
-    pl.a.chunk = 64;
-    pl.a.nseg = ceil_div(p.seqlen, pl.a.chunk);
-    pl.a.n_items = p.batch * p.dim * pl.a.nseg;
-    pl.blocks = ceil_div(pl.a.n_items, 256);
-    pl.records = pl.a.n_items;
-    return pl;
-}
-
-template <typename T, int W, bool SILU>
-int launch_plan(BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream) {
-    const dim3 grid((unsigned)pl.blocks);
-    BwdArgs& a = pl.a;
-    if (pl.kind == kBwdRows) {
-        if constexpr (W - 1 <= elems16<T>::value) {
-            return with_flag(p.seq_idx != nullptr, [&](auto qc) {
-                constexpr bool SEQ = decltype(qc)::value;
-                if (pl.vpt == 4) bwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
-                else if (pl.vpt == 2) bwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
-                else bwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 64 * kRowsWPB, 0, stream>>>(a);
-                return launch_status();
-            });
-        }
-        return CC1D_ERR_SHAPE;  // not reached: the plan only picks rows when the halo fits
-    }
-    if (pl.kind == kBwdCl) {
-        return with_flag(p.seq_idx != nullptr, [&](auto qc) {
-            constexpr bool SEQ = decltype(qc)::value;
-            constexpr int G = W - 1 <= kClG ? kClG : 2 * kClG;  // at least H steps per chunk
-            bwd_clw<T, W, G, kClR, kClWPB, SILU, SEQ><<<grid, 64 * kClWPB, 0, stream>>>(a);
-            return launch_status();
-        });
-    }
-    bwd_generic<T, W, SILU><<<grid, 256, 0, stream>>>(a);
-    return launch_status();
-}
-
-// Sum of the partial records of each channel, in a fixed order, written in
-// the dtype. Lanes run along the values of a record, so every load of a
-// wavefront reads 64 consecutive floats: value o of the outputs is (channel
-// o / (W+1), tap o % (W+1), the bias as tap W) for row and generic records,
-// whose (W+1) values per channel are contiguous, and value f of a channel
-// group's record (NC x W taps, then NC biases) for channel-last records.
-// Wavefront q of a block takes records q, q + waves, ... in that order, RB of
-// them in flight at a time, and the block adds its wavefronts' sums in LDS in
-// wavefront order. (With a lane per channel reading values 16-20 bytes
-// apart, C3's 10.5 MB of records took 8-10 us.)
-struct RedArgs {
-    const float* part;
-    void* dweight;
-    void* dbias;
-    int64_t dweight_stride[2];
-    int64_t dbias_stride;
-    int64_t batch, dim, nseg, groups;
-    int nc;           // cl: channels per record
-    int64_t nout;     // values reduced: dim * (W+1) (rows, generic) or groups * nc * (W+1) (cl)
-};
-
-template <typename T, int W, int KIND>
-__global__ void __launch_bounds__(1024) bwd_reduce(const RedArgs r) {
-    constexpr int RB = 8;  // records in flight per wavefront
-    __shared__ float acc[16][64];
-    const int lane = threadIdx.x & 63;
-    const int q = threadIdx.x >> 6;
-    const int nw = blockDim.x >> 6;
-    const int64_t o = (int64_t)blockIdx.x * 64 + lane;  // output value of this lane
-    const int64_t n = r.batch * r.nseg;                  // records per channel
-    const bool on = o < r.nout;
-    // channel, tap (W: bias) and the offset of this value in record j = (b, g)
-    int64_t c, k, grp = 0, f = 0;
-    if constexpr (KIND == kBwdCl) {
-        const int64_t rec = (int64_t)r.nc * (W + 1);
-        grp = o / rec;
-        f = o - grp * rec;
-        const bool tap = f < (int64_t)r.nc * W;
-        c = grp * r.nc + (tap ? f / W : f - (int64_t)r.nc * W);
-        k = tap ? f % W : W;
-    } else {
-        c = o / (W + 1);
-        k = o - c * (W + 1);
-    }
-    auto at = [&](int64_t j) -> const float* {
-        const int64_t b = j / r.nseg, g = j - b * r.nseg;
-        if constexpr (KIND == kBwdCl)
-            return r.part + ((b * r.nseg + g) * r.groups + grp) * (int64_t)r.nc * (W + 1) + f;
-        else if constexpr (KIND == kBwdRows)
-            return r.part + ((b * r.dim + c) * r.nseg + g) * (W + 1) + k;
-        else
-            return r.part + ((b * r.nseg + g) * r.dim + c) * (W + 1) + k;
-    };
-    float sum = 0.0f;
-    if (on) {
-        for (int64_t jb = q; jb < n; jb += (int64_t)nw * RB) {
-            float v[RB];
-#pragma unroll
-            for (int u = 0; u < RB; ++u) {
-                const int64_t j = jb + (int64_t)u * nw;
-                v[u] = j < n ? *at(j) : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < RB; ++u) sum += v[u];
-        }
-    }
-    acc[q][lane] = sum;
-    __syncthreads();
-    if (q == 0 && on && c < r.dim) {
-        float t = 0.0f;
-        for (int w = 0; w < nw; ++w) t += acc[w][lane];
-        if (k < W) st(static_cast<T*>(r.dweight), c * r.dweight_stride[0] + k * r.dweight_stride[1], t);
-        else if (r.dbias != nullptr) st(static_cast<T*>(r.dbias), c * r.dbias_stride, t);
-    }
-}
-
-}  // namespace
-
 int launch_bwd(const cc1d_bwd_params& p, hipStream_t stream) {
-    return with_dtype(p.dtype, [&](auto tag) {
-        using T = decltype(tag);
-        return with_width(p.width, [&](auto wc) {
-            constexpr int W = decltype(wc)::value;
-            return with_flag(p.apply_silu != 0, [&](auto sc) {
-                BwdPlan pl = plan_bwd<T, W>(p);
-                return launch_plan<T, W, decltype(sc)::value>(pl, p, stream);
-            });
-        });
-    });
+    return with_dtype(p.dtype, [&](auto tag) { return launch_bwd_dtype<decltype(tag)>(p, stream); });
+}
+
+int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream) {
+    return with_dtype(p.dtype, [&](auto tag) { return launch_bwd_typed_dtype<decltype(tag)>(p, g, stream); });
 }
 
 int64_t bwd_workspace_floats(const cc1d_bwd_params& p) {
     int64_t n = -1;
     with_dtype(p.dtype, [&](auto tag) {
-        using T = decltype(tag);
-        return with_width(p.width, [&](auto wc) {
-            const BwdPlan pl = plan_bwd<T, decltype(wc)::value>(p);
-            n = pl.records * pl.rec_floats;
-            return (int)CC1D_OK;
-        });
+        n = bwd_workspace_floats_dtype<decltype(tag)>(p);
+        return (int)CC1D_OK;
     });
     return n;
 }
@@ -1251,42 +80,6 @@ int launch_bwd_typed_noalloc(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, 
     gs.workspace = ws;
     gs.workspace_floats = kStaticWorkspaceFloats;
     return launch_bwd_typed(p, gs, stream);
-}
-
-int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream) {
-    return with_dtype(p.dtype, [&](auto tag) {
-        using T = decltype(tag);
-        return with_width(p.width, [&](auto wc) {
-            constexpr int W = decltype(wc)::value;
-            return with_flag(p.apply_silu != 0, [&](auto sc) {
-                BwdPlan pl = plan_bwd<T, W>(p);
-                if (pl.records * pl.rec_floats > g.workspace_floats) return (int)CC1D_ERR_WORKSPACE;
-                pl.a.part = g.workspace;
-                const int st = launch_plan<T, W, decltype(sc)::value>(pl, p, stream);
-                if (st != CC1D_OK) return st;
-                RedArgs r;
-                r.part = g.workspace;
-                r.dweight = g.dweight;
-                r.dbias = g.dbias;
-                r.dweight_stride[0] = g.dweight_stride[0];
-                r.dweight_stride[1] = g.dweight_stride[1];
-                r.dbias_stride = g.dbias_stride;
-                r.batch = p.batch;
-                r.dim = p.dim;
-                r.nseg = pl.a.nseg;
-                r.groups = pl.a.groups;
-                r.nc = 64 * (pl.cpl > 0 ? pl.cpl : 1);
-                r.nout = pl.kind == kBwdCl ? pl.a.groups * r.nc * (W + 1) : p.dim * (W + 1);
-                const int64_t n = p.batch * pl.a.nseg;  // records per channel
-                const dim3 grid((unsigned)ceil_div(r.nout, 64));
-                const unsigned threads = 64 * (unsigned)(n < 16 ? n : 16);
-                if (pl.kind == kBwdRows) bwd_reduce<T, W, kBwdRows><<<grid, threads, 0, stream>>>(r);
-                else if (pl.kind == kBwdCl) bwd_reduce<T, W, kBwdCl><<<grid, threads, 0, stream>>>(r);
-                else bwd_reduce<T, W, kBwdGeneric><<<grid, threads, 0, stream>>>(r);
-                return launch_status();
-            });
-        });
-    });
 }
 
 }  // namespace cc1d

@@ -1,0 +1,11 @@
+// cc1d_bwd_fp16.hip -- the backward kernels and launchers for f16 storage
+// (one translation unit per dtype, so the three compile in parallel).
+#include "cc1d_bwd_kernels.hpp"
+
+namespace cc1d {
+
+template int launch_bwd_dtype<f16>(const cc1d_bwd_params&, hipStream_t);
+template int launch_bwd_typed_dtype<f16>(const cc1d_bwd_params&, const cc1d_bwd_grads&, hipStream_t);
+template int64_t bwd_workspace_floats_dtype<f16>(const cc1d_bwd_params&);
+
+}  // namespace cc1d

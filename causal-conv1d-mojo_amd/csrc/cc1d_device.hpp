@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "cc1d_fastdiv.hpp"
+
 namespace cc1d {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -286,6 +288,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Wavefront-uniform value (lets the compiler keep it in an SGPR).
 __device__ __forceinline__ uint32_t uniform32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uniform_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
 __device__ __forceinline__ int64_t uniform(int64_t v) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));

@@ -28,6 +28,8 @@ namespace cc1d {
 
 struct FwdArgs {
     cc1d_fwd_params p;
+    FastDiv nseg_div;  // rows_vec: item -> row
+    FastDiv dim_div;   // rows_vec: row -> batch entry
     int64_t nseg;     // segments (rows_vec), tiles (cl) or chunks (generic) per row
     int64_t n_items;  // work items: segments / tiles / threads
     int64_t chunk;    // time steps per item (cl / generic)
@@ -158,12 +160,11 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
     const int lane = threadIdx.x & 63;
     const uint32_t item = uniform32(blockIdx.x * 4u + (threadIdx.x >> 6));
     if (item >= (uint32_t)a.n_items) return;
-    const uint32_t nseg = (uint32_t)a.nseg;
-    const uint32_t row = item / nseg;
-    const int32_t t0 = (int32_t)((item - row * nseg) * SEG);
-    const uint32_t dim = (uint32_t)p.dim;
-    const uint32_t b = row / dim;
-    const uint32_t c = row - b * dim;
+    // (row, segment) and (b, c) by the host's invariant-divisor constants
+    const uint32_t row = a.nseg_div.div(item);
+    const int32_t t0 = (int32_t)((item - row * (uint32_t)a.nseg) * SEG);
+    const uint32_t b = a.dim_div.div(row);
+    const uint32_t c = row - b * (uint32_t)p.dim;
     if (t0 + SEG <= (int32_t)p.seqlen) fwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0);
     else fwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0);
 }
@@ -437,13 +438,14 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
+                        a.nseg_div = FastDiv((uint32_t)a.nseg);
+                        a.dim_div = FastDiv((uint32_t)p.dim);
                         const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                             constexpr bool SEQ = decltype(qc)::value;
-                            if (vpt == 4) fwd_rows_vec<T, W, 4, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                            else if (vpt == 2) fwd_rows_vec<T, W, 2, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                            else fwd_rows_vec<T, W, 1, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                            return launch_status();
+                            if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ>, grid, dim3(256), stream, a);
+                            if (vpt == 2) return launch(fwd_rows_vec<T, W, 2, SILU, SEQ>, grid, dim3(256), stream, a);
+                            return launch(fwd_rows_vec<T, W, 1, SILU, SEQ>, grid, dim3(256), stream, a);
                         });
                     }
                 }
@@ -456,16 +458,14 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                     const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                     return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                         constexpr bool SEQ = decltype(qc)::value;
-                        fwd_cl<T, W, CPL, kClTS, SILU, SEQ><<<grid, 256, 0, stream>>>(a);
-                        return launch_status();
+                        return launch(fwd_cl<T, W, CPL, kClTS, SILU, SEQ>, grid, dim3(256), stream, a);
                     });
                 }
                 a.chunk = 64;
                 a.nseg = ceil_div(p.seqlen, a.chunk);
                 a.n_items = rows * a.nseg;
                 const dim3 grid((unsigned)ceil_div(a.n_items, 256));
-                fwd_generic<T, W, SILU><<<grid, 256, 0, stream>>>(a);
-                return launch_status();
+                return launch(fwd_generic<T, W, SILU>, grid, dim3(256), stream, a);
             });
         });
     });

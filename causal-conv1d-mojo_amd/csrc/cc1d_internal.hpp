@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <tuple>
 #include <type_traits>
 
 #include "cc1d.h"
@@ -21,6 +22,11 @@ int launch_bwd_typed(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStrea
 int launch_bwd_typed_noalloc(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream);
 constexpr int64_t kStaticWorkspaceFloats = CC1D_NOALLOC_WORKSPACE_FLOATS;
 int64_t bwd_workspace_floats(const cc1d_bwd_params& p);
+// per-dtype backward launchers (explicitly instantiated in cc1d_bwd_<dtype>.hip)
+template <typename T> int launch_bwd_dtype(const cc1d_bwd_params& p, hipStream_t stream);
+template <typename T>
+int launch_bwd_typed_dtype(const cc1d_bwd_params& p, const cc1d_bwd_grads& g, hipStream_t stream);
+template <typename T> int64_t bwd_workspace_floats_dtype(const cc1d_bwd_params& p);
 int launch_update(const cc1d_update_params& p, hipStream_t stream);
 int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream);
 // element size of a varlen gather: elem_bytes, or the size of dtype when it is 0
@@ -54,8 +60,24 @@ template <typename F> int with_flag(bool flag, F&& f) {
     return flag ? f(std::true_type{}) : f(std::false_type{});
 }
 
-inline int launch_status() {
-    return hipGetLastError() == hipSuccess ? CC1D_OK : CC1D_ERR_LAUNCH;
+// Launches kernel k with the given arguments (converted to its parameter
+// types) and returns the status of this launch alone: hipLaunchKernel reports
+// it directly, so an error that an earlier, unrelated call left on the thread
+// is neither returned as ours nor cleared. A failed launch's own error is
+// taken off the thread, so it does not surface in the caller's next check.
+template <typename... P, typename... A>
+int launch(void (*k)(P...), dim3 grid, dim3 block, hipStream_t stream, const A&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "one argument per kernel parameter");
+    std::tuple<std::decay_t<P>...> vals(args...);
+    void* ptrs[sizeof...(P)];
+    std::apply([&](auto&... v) {
+        int i = 0;
+        ((ptrs[i++] = static_cast<void*>(&v)), ...);
+    }, vals);
+    const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(k), grid, block, ptrs, 0, stream);
+    if (e == hipSuccess) return CC1D_OK;
+    (void)hipGetLastError();
+    return CC1D_ERR_LAUNCH;
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

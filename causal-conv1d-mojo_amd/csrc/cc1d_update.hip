@@ -335,8 +335,10 @@ __global__ void __launch_bounds__(64 * WPG) update_dir(const LinArgs<T> a) {
         for (int q = 0; q < BPW; ++q)
             row[q] = (r[q] < 0 || r[q] >= a.state_rows) ? -1 : r[q];  // padding (any negative) or out of the pool
     } else {
+        // without indices, entry b uses row b; an entry past the batch (odd
+        // batch, last wavefront) reads row nb-1, in bounds, and stores nothing
 #pragma unroll
-        for (int q = 0; q < BPW; ++q) row[q] = (int32_t)(b0 + q);
+        for (int q = 0; q < BPW; ++q) row[q] = (int32_t)min(b0 + q, nb - 1);
     }
     uint32_t st[BPW][NS][H];
 #pragma unroll
@@ -738,9 +740,9 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                                       (unsigned)ceil_div(p.batch, kDirBPW));
                         return with_flag(p.bias != nullptr, [&](auto hb) {
                             return with_flag(p.conv_state_indices != nullptr, [&](auto hi) {
-                                update_dir<T, W, kDirBPW, kDirNS, kDirWPG, SILU, decltype(hb)::value, decltype(hi)::value>
-                                    <<<gd, 64 * kDirWPG, 0, stream>>>(la);
-                                return launch_status();
+                                return launch(update_dir<T, W, kDirBPW, kDirNS, kDirWPG, SILU, decltype(hb)::value,
+                                                         decltype(hi)::value>,
+                                              gd, dim3(64 * kDirWPG), stream, la);
                             });
                         });
                     }
@@ -748,9 +750,8 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                     const dim3 grid((unsigned)ceil_div(p.dim, 16 * EPV * kLinNV), (unsigned)p.batch);
                     return with_flag(p.bias != nullptr, [&](auto hb) {
                         return with_flag(p.conv_state_indices != nullptr, [&](auto hi) {
-                            update_lin<T, W, kLinNV, SILU, decltype(hb)::value, decltype(hi)::value>
-                                <<<grid, 64, 0, stream>>>(la);
-                            return launch_status();
+                            return launch(update_lin<T, W, kLinNV, SILU, decltype(hb)::value, decltype(hi)::value>,
+                                          grid, dim3(64), stream, la);
                         });
                     });
                 }
@@ -760,20 +761,17 @@ int launch_update(const cc1d_update_params& p, hipStream_t stream) {
                     if (circ_vec_ok<T>(p)) {
                         a.n_items = 2 * p.batch * p.dim;  // two lanes per (b, c)
                         return with_flag(circ_dwords_ok<T>(p), [&](auto dc) {
-                            update_circ_vec<T, W, SILU, decltype(dc)::value>
-                                <<<dim3((unsigned)ceil_div(a.n_items, 256)), 256, 0, stream>>>(a);
-                            return launch_status();
+                            return launch(update_circ_vec<T, W, SILU, decltype(dc)::value>,
+                                          dim3((unsigned)ceil_div(a.n_items, 256)), dim3(256), stream, a);
                         });
                     }
                 }
                 if (p.cache_seqlens != nullptr && p.seqlen <= 8) {
-                    update_circ<T, W, SILU, 8><<<grid, 256, 0, stream>>>(a);
-                    return launch_status();
+                    return launch(update_circ<T, W, SILU, 8>, grid, dim3(256), stream, a);
                 }
                 return with_flag(p.cache_seqlens != nullptr, [&](auto cc) {
                     constexpr bool CIRC = decltype(cc)::value;
-                    update_generic<T, W, SILU, CIRC><<<grid, 256, 0, stream>>>(a);
-                    return launch_status();
+                    return launch(update_generic<T, W, SILU, CIRC>, grid, dim3(256), stream, a);
                 });
             });
         });

@@ -57,14 +57,13 @@ int launch_varlen_states(const cc1d_varlen_params& p, hipStream_t stream) {
     a.n_items = p.batch * p.state_len * p.dim;
     const dim3 grid((unsigned)ceil_div(a.n_items, 256));
     switch (varlen_elem_bytes(p)) {
-    case 1: varlen_states_kernel<1><<<grid, 256, 0, stream>>>(a); break;
-    case 2: varlen_states_kernel<2><<<grid, 256, 0, stream>>>(a); break;
-    case 4: varlen_states_kernel<4><<<grid, 256, 0, stream>>>(a); break;
-    case 8: varlen_states_kernel<8><<<grid, 256, 0, stream>>>(a); break;
-    case 16: varlen_states_kernel<16><<<grid, 256, 0, stream>>>(a); break;
+    case 1: return launch(varlen_states_kernel<1>, grid, dim3(256), stream, a);
+    case 2: return launch(varlen_states_kernel<2>, grid, dim3(256), stream, a);
+    case 4: return launch(varlen_states_kernel<4>, grid, dim3(256), stream, a);
+    case 8: return launch(varlen_states_kernel<8>, grid, dim3(256), stream, a);
+    case 16: return launch(varlen_states_kernel<16>, grid, dim3(256), stream, a);
     default: return CC1D_ERR_DTYPE;
     }
-    return launch_status();
 }
 
 template <typename U>
@@ -85,12 +84,10 @@ int launch_zero3(void* ptr, int esize, int64_t n0, int64_t n1, int64_t n2, const
     if (n == 0) return CC1D_OK;
     const dim3 grid((unsigned)ceil_div(n, 256));
     if (esize == 2)
-        zero3_kernel<uint16_t><<<grid, 256, 0, stream>>>(static_cast<uint16_t*>(ptr), n0, n1, n2, stride[0],
-                                                         stride[1], stride[2]);
-    else
-        zero3_kernel<uint32_t><<<grid, 256, 0, stream>>>(static_cast<uint32_t*>(ptr), n0, n1, n2, stride[0],
-                                                         stride[1], stride[2]);
-    return launch_status();
+        return launch(zero3_kernel<uint16_t>, grid, dim3(256), stream, static_cast<uint16_t*>(ptr), n0, n1, n2,
+                      stride[0], stride[1], stride[2]);
+    return launch(zero3_kernel<uint32_t>, grid, dim3(256), stream, static_cast<uint32_t*>(ptr), n0, n1, n2,
+                  stride[0], stride[1], stride[2]);
 }
 
 }  // namespace cc1d

@@ -63,3 +63,30 @@ def test_channel_last_batch_beyond_2_31_elements():
     assert_reduction_close(dw[chans].cpu(), rdw, torch.bfloat16, scale=sw, name="dweight")
     del base, x, out, dout
     torch.cuda.empty_cache()
+
+
+def test_channel_last_fp32_batch_of_2_30_elements():
+    """fp32 channel-last with 2^30 <= L * D < 2^31 elements in one batch entry: element offsets
+    fit in 32 bits but byte offsets do not, so the backward must not form 32-bit byte offsets
+    (positions past 2^32 / (4 D) would alias earlier rows)."""
+    B, L, D, W = 1, 140000, 8192, 4
+    assert 2 ** 30 <= L * D < 2 ** 31
+    g = torch.Generator(device=DEV).manual_seed(2)
+    base = torch.randn(B, L, D, generator=g, device=DEV, dtype=torch.float32)
+    w = torch.randn(D, W, generator=g, device=DEV, dtype=torch.float32)
+    x = base.transpose(1, 2)
+    xg = x.detach().requires_grad_()
+    wg = w.clone().requires_grad_()
+    out = cc.causal_conv1d_fn(xg, wg, None, activation="silu")
+    chans = torch.tensor([0, D // 2 + 1, D - 1])
+    xs, ws = _sample(x, chans), w[chans].cpu()
+    assert_close(_sample(out.detach(), chans), O.causal_conv1d_fn(xs, ws, None, activation="silu"),
+                 torch.float32)
+    dout = torch.randn(B, L, D, generator=g, device=DEV, dtype=torch.float32).transpose(1, 2)
+    dx, dw = torch.autograd.grad(out, (xg, wg), dout)
+    rdx, rdw, _, _ = O.causal_conv1d_bwd(xs, ws, None, _sample(dout, chans), activation="silu")
+    assert_close(_sample(dx, chans), rdx, torch.float32, name="dx")
+    sw, _ = scales(xs, ws, None, _sample(dout, chans), activation="silu")
+    assert_reduction_close(dw[chans].cpu(), rdw, torch.float32, scale=sw, name="dweight")
+    del base, x, xg, out, dout, dx
+    torch.cuda.empty_cache()

@@ -196,11 +196,11 @@ def test_padding_and_out_of_pool_rows(dtype, dim, circular):
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("width", [2, 3, 4, 5])
-@pytest.mark.parametrize("dim", [130, 200])  # a partial last channel group
+@pytest.mark.parametrize("dim", [136, 200])  # whole 16-byte vectors, a partial last channel group
 def test_odd_batch_offset_indices(dtype, width, dim):
     """Two batch entries per wavefront with an odd batch (the last wavefront's second entry is
     past the end), indices read from a view at a 4-byte (not 8-byte) aligned address, and a
-    channel group that ends inside a wavefront."""
+    channel group that ends inside a wavefront (both dims take the direct decode kernel)."""
     B, P = 7, 9
     full = torch.tensor([99, 3, 0, -1, 8, 5, -3, 1], dtype=torch.int32)
     idx = full.to(DEV)[1:]  # storage offset of one int32
@@ -220,6 +220,24 @@ def test_odd_batch_offset_indices(dtype, width, dim):
     assert_equal(st[ids[real].long()], rs)
     untouched = [r for r in range(P) if r not in ids.tolist()]
     assert_equal(st[untouched], pool[untouched])
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("batch", [1, 7])
+def test_odd_batch_without_indices_exact_state(dtype, batch):
+    """Batch entry b updates state row b; with an odd batch the last wavefront's second entry
+    lies past the batch and must neither store nor read beyond the last state row (the state
+    tensor here has exactly `batch` rows)."""
+    D, W = 264, 4
+    x, w, b, _ = make_inputs(batch, D, 1, W, dtype=dtype)
+    state = make_inputs(batch, D, W - 1, W, dtype=dtype, seed=1)[0]
+    sg = state.to(DEV)
+    og = torch.full((batch, D, 1), float("nan"), dtype=dtype, device=DEV)
+    native_update(x.to(DEV), w.to(DEV), b.to(DEV), sg, None, None, og, True)
+    rs = state.clone()
+    rout = O.causal_conv1d_update(x[:, :, 0], rs, w, b, activation="silu")
+    assert_close(og[..., 0].cpu(), rout, dtype)
+    assert_equal(sg.cpu(), rs)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
