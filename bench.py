@@ -183,7 +183,7 @@ class Floors:
         i64, i32, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
         lib.cc1d_floor_copy.argtypes = [vp, vp, i64, vp]
         lib.cc1d_floor_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i32, vp]
-        lib.cc1d_floor_chunks.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, vp]
+        lib.cc1d_floor_chunks.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, i32, i32, vp]
         lib.cc1d_floor_tiles.argtypes = [vp, vp, vp, i64, i64, i32, vp]
         lib.cc1d_floor_walk.argtypes = [vp, vp, vp, i64, i64, vp]
         for f in (lib.cc1d_floor_copy, lib.cc1d_floor_rows, lib.cc1d_floor_chunks, lib.cc1d_floor_tiles,
@@ -219,13 +219,15 @@ class Floors:
                                              x.shape[1] * x.element_size(), torch.cuda.current_stream().cuda_stream),
                     "cc1d_floor_walk")
 
-    def chunks(self, torch, x, out, pool, idx, cs, nchunks):
+    def chunks(self, torch, x, out, pool, idx, cs, nchunks, gran=1):
+        """gran 1: the nchunks 16-byte chunks; 4 / 8: the whole 64-byte sectors / 128-byte lines
+        holding them"""
         line_chunks = pool.shape[2] * pool.element_size() // 16
         xwords = x.shape[2] * x.element_size() // 4
         self._check(self.lib.cc1d_floor_chunks(x.data_ptr(), out.data_ptr(), pool.data_ptr(), idx.data_ptr(),
                                                cs.data_ptr(), x.shape[0], x.shape[1], line_chunks,
                                                pool[0].numel() * pool.element_size() // 16, pool.shape[0],
-                                               nchunks, xwords, torch.cuda.current_stream().cuda_stream),
+                                               nchunks, xwords, gran, torch.cuda.current_stream().cuda_stream),
                     "cc1d_floor_chunks")
 
 
@@ -328,6 +330,35 @@ def _c2_cases(torch, sets, w, b):
     }
 
 
+def _c2_seq_cases(torch, sets, w, b):
+    """C2's shape with seq_idx: every batch row packs 8 sequences of random lengths (7 uniform
+    split points, C3's pattern), so each row's kernels run the id-gated arithmetic."""
+    ops = torch.ops.causal_conv1d_amd
+    g = torch.Generator().manual_seed(5)
+    seq = torch.zeros(B, L, dtype=torch.int32)
+    for r in range(B):
+        cuts = torch.sort(torch.randperm(L - 1, generator=g)[:7] + 1).values
+        for i, c in enumerate(cuts.tolist()):
+            seq[r, c:] = i + 1
+    seq = seq.cuda()
+    dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
+    db = torch.zeros(D, dtype=torch.float32, device="cuda")
+    dwt = torch.empty(D, W, dtype=torch.bfloat16, device="cuda")
+    dbt = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    bufs = [(x.detach(), dout, torch.empty_like(x), torch.empty_like(x)) for x, dout in sets]
+    sb = B * L * 4
+    note = {"workload": "C2 shape (4 x 5120 x 2048 bf16, W4, bias, SiLU) with seq_idx: 8 sequences per row"}
+    return {
+        "fwd_seq": ([lambda x=x, o=o: ops._fwd_inplace(x, w, b, seq, None, o, True, None) for x, _, o, _ in bufs],
+                    FWD_BYTES + sb, 1, note),
+        "bwd_seq": ([lambda x=x, d=d, dx=dx: ops._bwd_full_inplace(x, w, b, d, seq, None, dx, dw, db, None, True)
+                     for x, d, _, dx in bufs], BWD_BYTES + sb, 1, note),
+        "bwd_typed_seq": ([lambda x=x, d=d, dx=dx: ops._bwd_typed_inplace(x, w, b, d, seq, None, None, dx, dwt, dbt,
+                                                                           None, True)
+                           for x, d, _, dx in bufs], BWD_TYPED_BYTES + sb, 1, note),
+    }
+
+
 def _c2_floor_cases(torch, sets, floors):
     """The C2 backward's streams with no arithmetic: x and dout read, dx written, on the
     same sets viewed as (B * D) rows of 4 KB: a wavefront per 4 rows x 1 KB, or per row
@@ -379,6 +410,9 @@ def _c4a_cases(torch, cc, floors):
                torch.empty(half, dtype=torch.uint8, device="cuda")) for _ in range(nsets)]
         cases["floor_copy_c4a"] = ([lambda a=a, c=c: floors.copy(torch, a, c) for a, c in cp], 2 * half, 1,
                                    {"note": "plain copy of the update's bytes, one 16-byte vector per lane"})
+        cases["runtime_copy_c4a"] = ([lambda a=a, c=c: c.copy_(a) for a, c in cp], 2 * half, 1,
+                                     {"note": "the runtime's own device-to-device copy (torch copy_, a memcpy node "
+                                              "in the graph) of the same bytes"})
         cases["floor_rows_c4a"] = ([lambda u=u: floors.rows(torch, u[0][..., 0], u[4][..., 0], u[1], u[2], W - 1)
                                     for u in sets], UPD_BYTES, 1,
                                    {"note": "the update's scattered rows without arithmetic: x row and pool row "
@@ -483,6 +517,12 @@ def _c4b_cases(torch, cc, floors):
                 [lambda u=u, nch=nch: floors.chunks(torch, u[0], u[4], u[1], u[2], u[3], nch) for u in sets],
                 C4B_BYTES, 1, {"note": f"{nch} 16-byte chunk(s) of each state line read and written back, x / out "
                                        "moved, no arithmetic"})
+        for gran, name in ((4, "sector"), (8, "line")):
+            cases[f"floor_{name}_c4b"] = (
+                [lambda u=u, gran=gran: floors.chunks(torch, u[0], u[4], u[1], u[2], u[3], 2, gran) for u in sets],
+                C4B_BYTES, 1, {"note": f"the whole aligned {16 * gran}-byte granule(s) holding two 16-byte chunks "
+                                       "of each state line read and written back (no partial granule written), "
+                                       "x / out moved, no arithmetic"})
     return cases, hbm
 
 
@@ -537,6 +577,8 @@ def bench_configs(torch, cc, floors, args):
     if "floor_chunks2_c4b" in res:
         e["floor_chunks1_us"] = res["floor_chunks1_c4b"]["us_per_launch"]
         e["floor_chunks2_us"] = res["floor_chunks2_c4b"]["us_per_launch"]
+        e["floor_sector_us"] = res["floor_sector_c4b"]["us_per_launch"]
+        e["floor_line_us"] = res["floor_line_c4b"]["us_per_launch"]
     del c4b
     torch.cuda.empty_cache()
     _run_cases(torch, _varlen_case(torch, cc, c3info), args, res)
@@ -636,6 +678,7 @@ def mode_kernels(torch, cc, floors, args):
     cases.update(_c2_floor_cases(torch, sets, floors))
     cases.update(_c4a_cases(torch, cc, floors))
     if not args.no_configs:
+        cases.update(_c2_seq_cases(torch, sets, w, b))
         c3, c3info = _c3_cases(torch, floors)
         cases.update(c3)
         cases.update(_c5_cases(torch))
@@ -685,6 +728,8 @@ def main():
     kern = {}
     _run_cases(torch, _c2_cases(torch, sets, w, b), args, kern)
     _run_cases(torch, _c2_floor_cases(torch, sets, floors), args, kern)
+    if not args.no_configs:
+        _run_cases(torch, _c2_seq_cases(torch, sets, w, b), args, kern)
     for k in ("fwd", "bwd", "bwd_typed"):
         kern[k]["buffer_sets"] = nsets
     kern["fwd"]["floor_copy_us"] = kern["floor_copy_c2"]["us_per_launch"]
@@ -699,6 +744,7 @@ def main():
     u["us_per_call_cache_resident"] = kern.pop("update_c4a_cache_resident")["us_per_launch"]
     u["floor_copy_us"] = kern["floor_copy_c4a"]["us_per_launch"]
     u["floor_rows_us"] = kern["floor_rows_c4a"]["us_per_launch"]
+    u["runtime_copy_us"] = kern["runtime_copy_c4a"]["us_per_launch"]
     torch.cuda.empty_cache()
     if not args.no_configs:
         kern.update(bench_configs(torch, cc, floors, args))

@@ -36,7 +36,11 @@
 //                        read and write back `chunks` consecutive 16-byte
 //                        chunks of state line (idx[b], c) starting at chunk
 //                        cs[b] mod line_chunks (wrapping), and read x / write
-//                        out `xwords` dwords.
+//                        out `xwords` dwords. With gran > 1 the whole aligned
+//                        granules of gran chunks (4: the 64-byte sectors, 8:
+//                        the 128-byte line) that hold those chunks are read
+//                        and written back instead, so no partial granule is
+//                        written.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -91,7 +95,7 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
                                                     u32x4* __restrict__ pool, const int32_t* __restrict__ idx,
                                                     const int32_t* __restrict__ cs, int64_t batch, int64_t dim,
                                                     int64_t line_chunks, int64_t pool_row_chunks, int64_t pool_rows,
-                                                    int chunks, int xwords) {
+                                                    int chunks, int xwords, int gran) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= batch * dim) return;
     const int64_t b = t / dim;
@@ -103,10 +107,21 @@ __global__ void __launch_bounds__(256) floor_chunks(const uint32_t* __restrict__
     int64_t k = cs[b] % line_chunks;
     if (k < 0) k += line_chunks;
     u32x4* line = pool + (int64_t)row * pool_row_chunks + c * line_chunks;
-    u32x4 v[2];
-    for (int j = 0; j < chunks; ++j) v[j] = line[(k + j) % line_chunks];
+    // the chunks moved: [k, k + chunks), or the granules of gran chunks holding them
+    int n = chunks;
+    if (gran > 1) {
+        const bool two = gran < line_chunks && (k % gran) + chunks > gran;
+        k -= k % gran;
+        n = two ? 2 * gran : gran;
+    }
+    u32x4 v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < n) v[j] = line[(k + j) % line_chunks];
     for (int i = 0; i < xwords; ++i) __builtin_nontemporal_store(xv[i] ^ 1u, &out[t * xwords + i]);
-    for (int j = 0; j < chunks; ++j) line[(k + j) % line_chunks] = flip(v[j]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        if (j < n) line[(k + j) % line_chunks] = flip(v[j]);
 }
 
 // grid: (slices per row) x (row tiles / 4), 4 wavefronts per block on
@@ -265,18 +280,20 @@ int cc1d_floor_walk(const void* x, const void* g, void* out, int64_t rows, int64
 
 // pool: pool_rows rows of pool_row_chunks 16-byte chunks, dim lines of
 // line_chunks chunks each; x, out: (batch, dim) items of xwords dwords; chunks
-// in {1, 2}; xwords in 1..4; idx entries outside [0, pool_rows) are skipped
+// in {1, 2}; xwords in 1..4; gran 1 (the chunks themselves) or 4 / 8 (whole
+// granules, dividing line_chunks, at most 8); idx entries outside
+// [0, pool_rows) are skipped
 int cc1d_floor_chunks(const void* x, void* out, void* pool, const int32_t* idx, const int32_t* cs, int64_t batch,
                       int64_t dim, int64_t line_chunks, int64_t pool_row_chunks, int64_t pool_rows, int chunks,
-                      int xwords, void* stream) {
+                      int xwords, int gran, void* stream) {
     if (batch < 0 || dim < 0 || line_chunks < 2 || chunks < 1 || chunks > 2 || xwords < 1 || xwords > 4 ||
-        pool_row_chunks < dim * line_chunks)
+        pool_row_chunks < dim * line_chunks || (gran != 1 && gran != 4 && gran != 8) || line_chunks % gran)
         return -1;
     if (batch == 0 || dim == 0) return 0;
     if (x == nullptr || out == nullptr || pool == nullptr || idx == nullptr || cs == nullptr) return -1;
     floor_chunks<<<dim3((unsigned)((batch * dim + 255) / 256)), 256, 0, static_cast<hipStream_t>(stream)>>>(
         static_cast<const uint32_t*>(x), static_cast<uint32_t*>(out), static_cast<u32x4*>(pool), idx, cs, batch, dim,
-        line_chunks, pool_row_chunks, pool_rows, chunks, xwords);
+        line_chunks, pool_row_chunks, pool_rows, chunks, xwords, gran);
     return launched() ? 0 : -2;
 }
 

@@ -52,8 +52,8 @@ def test_rows_floor(floors, dim):
         assert torch.equal(pool[r], want), f"pool row {r}"
 
 
-@pytest.mark.parametrize("nchunks", [1, 2])
-def test_chunks_floor(floors, nchunks):
+@pytest.mark.parametrize("nchunks,gran", [(1, 1), (2, 1), (1, 4), (2, 4), (2, 8)])
+def test_chunks_floor(floors, nchunks, gran):
     B, D, S, L, P = 5, 48, 64, 4, 7
     g = torch.Generator(device=DEV).manual_seed(1)
     x = torch.randn(B, D, L, generator=g, device=DEV).bfloat16()
@@ -62,15 +62,20 @@ def test_chunks_floor(floors, nchunks):
     idx = torch.tensor([6, 1, 3, 0, 4], dtype=torch.int32, device=DEV)
     cs = torch.tensor([0, 7, 63, -1, 20], dtype=torch.int32, device=DEV)
     before = pool.clone()
-    floors.chunks(torch, x, out, pool, idx, cs, nchunks)
+    floors.chunks(torch, x, out, pool, idx, cs, nchunks, gran)
     torch.cuda.synchronize()
     assert torch.equal(out, _flip(x))
     line_chunks = S * 2 // 16
     want = before.clone().view(P, D, line_chunks, 8)
     for b, (r, c) in enumerate(zip(idx.tolist(), cs.tolist())):
-        for j in range(nchunks):
-            k = (c % line_chunks + j) % line_chunks
-            want[r, :, k] = _flip(want[r, :, k])
+        k = c % line_chunks
+        if gran == 1:
+            ks = [(k + j) % line_chunks for j in range(nchunks)]
+        else:  # the whole granules holding chunks k .. k + nchunks - 1
+            two = gran < line_chunks and k % gran + nchunks > gran
+            ks = [(k - k % gran + j) % line_chunks for j in range(2 * gran if two else gran)]
+        for kk in ks:
+            want[r, :, kk] = _flip(want[r, :, kk])
     assert torch.equal(pool, want.view(P, D, S))
 
 
