@@ -331,6 +331,195 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
     }
 }
 
+// The seq_idx form of bwd_rows_compute (seq_idx excludes initial_states,
+// dfinal_states and dinitial_states, so none of those appear). dx is
+// scattered instead of gathered: the gates of position s -- tap k is kept
+// when seq_idx[s - k] == seq_idx[s] -- are compared once, while s's dpre is
+// computed, and used at once for the SiLU argument, the weight-gradient
+// sums and s's contributions w[W-1-k] * dpre[s] to dx[s - k]. No gate is
+// kept beyond its position (a gather compares each pair a second time, for
+// dx, and keeps the comparisons or the ids of both sides until then).
+// Contributions to the H positions before the lane's first collect in a
+// carry that the owning lane fetches from its neighbour (lane 63: from lane
+// 0 of the next vector, or from the next segment's first H positions); each
+// dx sum is the gather's fma chain with that carry added as one term.
+template <typename T, int W, int VPT, bool SILU, bool FULL>
+__device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
+                                                     int32_t t0, const RowTile<VPT>& r, const float* w,
+                                                     const float* wq, float bq, float* pw, float& pb) {
+    constexpr int EPV = elems16<T>::value;
+    constexpr int H = W - 1;
+    constexpr int SEG = 64 * VPT * EPV;
+    static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
+    constexpr int D0 = ((EPV - H) * (int)sizeof(T)) / 4;
+    const int32_t L = (int32_t)p.seqlen;
+    const int32_t tn = t0 + SEG;  // first position of the next segment
+    T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
+    const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
+    const int prev_lane = (lane + 63) & 63;
+    const int next_lane = (lane + 1) & 63;
+
+    // ids: the lane's positions (-1 past the row end), and the H before and
+    // after the segment (wave-uniform, -1 outside the row)
+    int32_t id[VPT][EPV];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
+#pragma unroll
+        for (int q = 0; q < EPV / 4; ++q) {
+            const u32x4 sv = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                                             : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) id[j][4 * q + e] = (int32_t)sv[e];
+        }
+    }
+    int32_t hid[H], nid[H];
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+        hid[i] = t0 - H + i >= 0 ? ld_uniform(sr + (t0 - H + i)) : -1;
+        nid[i] = tn + i < L ? ld_uniform(sr + (tn + i)) : -1;
+    }
+
+    float acc[2][EPV];  // dx sums of the lane's positions, by vector parity
+    float carry[2][H];  // contributions to the H positions before the lane's first
+
+    // dx of vector j: add the carries for its last H positions (from the next
+    // lane's vector j; lane 63: `nxt`, lane 0's carry of vector j + 1, or with
+    // `local` the next segment's contributions computed by every lane) and store
+    auto finish = [&](const int j, float* a, const float* cj, const float* nxt, const bool local) {
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float send = (lane == 0 && !local) ? nxt[i] : cj[i];
+            float rv = lane_get(send, next_lane);
+            if (local && lane == 63) rv = nxt[i];
+            a[EPV - H + i] += rv;
+        }
+        if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(a));
+    };
+
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int32_t t = t0 + (j * 64 + lane) * EPV;
+        // x and id windows: the H positions before the vector, then its EPV
+        u32x4 pv = vzero();
+#pragma unroll
+        for (int d = D0; d < 4; ++d) {
+            const uint32_t send = (lane == 63) ? (j > 0 ? r.v[j > 0 ? j - 1 : 0][d] : 0u) : r.v[j][d];
+            pv[d] = lane_get(send, prev_lane);
+        }
+        if (j == 0 && lane == 0) pv = r.h;
+        float win[H + EPV];
+        int32_t iw[H + EPV];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            win[i] = vget<T>(pv, EPV - H + i);
+            const int32_t send = (lane == 63) ? (j > 0 ? id[j > 0 ? j - 1 : 0][EPV - H + i] : -1)
+                                              : id[j][EPV - H + i];
+            const int32_t rv = lane_get(send, prev_lane);
+            iw[i] = (j == 0 && lane == 0) ? hid[i] : rv;
+        }
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) {
+            win[H + i] = vget<T>(r.v[j], i);
+            iw[H + i] = id[j][i];
+        }
+        float* a = acc[j & 1];
+        float* cr = carry[j & 1];
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) a[i] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < H; ++i) cr[i] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            const int32_t cur = iw[H + e];
+            // tap kk of position s covers s - (H - kk): kept when the ids match
+            bool keep[W];
+            float xe[W];
+#pragma unroll
+            for (int kk = 0; kk < H; ++kk) {
+                keep[kk] = iw[e + kk] == cur;
+                xe[kk] = keep[kk] ? win[e + kk] : 0.0f;
+            }
+            keep[H] = true;
+            xe[H] = win[H + e];
+            const float g = vget<T>(r.gv[j], e);
+            float d = g;
+            if constexpr (SILU) {
+                float q = bq;
+#pragma unroll
+                for (int kk = 0; kk < W; ++kk) q = __builtin_fmaf(wq[kk], xe[kk], q);
+                d = silu_bwd_q(g, q);
+            }
+            if (!FULL && t + e >= L) d = 0.0f;
+            if (cur < 0) d = 0.0f;
+            pb += d;
+#pragma unroll
+            for (int kk = 0; kk < W; ++kk) pw[kk] = __builtin_fmaf(d, xe[kk], pw[kk]);
+            // dx[s - k] += w[W-1-k] * dpre[s] where tap W-1-k of s is kept
+#pragma unroll
+            for (int k = 0; k <= H; ++k) {
+                const float de = keep[H - k] ? d : 0.0f;
+                if (e - k >= 0) a[e - k] = __builtin_fmaf(w[W - 1 - k], de, a[e - k]);
+                else cr[H + e - k] = __builtin_fmaf(w[W - 1 - k], de, cr[H + e - k]);
+            }
+            // one position at a time: the sums are updated here (the compiler
+            // would otherwise sink their fmas to the end, keeping every
+            // position's gated window alive until then)
+#pragma unroll
+            for (int kk = 0; kk < W; ++kk) asm volatile("" : "+v"(pw[kk]));
+            asm volatile("" : "+v"(pb));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (j > 0) finish(j - 1, acc[(j - 1) & 1], carry[(j - 1) & 1], carry[j & 1], false);
+    }
+
+    // contributions of the next segment's first H positions to this segment's
+    // last H (lane 63's; zero when this segment ends the row)
+    float cn[H];
+#pragma unroll
+    for (int i = 0; i < H; ++i) cn[i] = 0.0f;
+    if (tn < L) {
+        float xw[2 * H];
+        int32_t iw[2 * H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            xw[i] = vget<T>(r.v[VPT - 1], EPV - H + i);
+            xw[H + i] = vget<T>(r.xn, i);
+            iw[i] = id[VPT - 1][EPV - H + i];
+            iw[H + i] = nid[i];
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < H; ++s2) {
+            const int32_t cur = iw[H + s2];
+            const float g = vget<T>(r.gn, s2);
+            float d = g;
+            if constexpr (SILU) {
+                float q = bq;
+#pragma unroll
+                for (int kk = 0; kk < W; ++kk) {
+                    const bool keep = kk == H || iw[s2 + kk] == cur;
+                    q = __builtin_fmaf(wq[kk], keep ? xw[s2 + kk] : 0.0f, q);
+                }
+                d = silu_bwd_q(g, q);
+            }
+            if (tn + s2 >= L || cur < 0) d = 0.0f;
+            // to the positions before tn: k = s2 + 1 .. H, position index H + s2 - k
+#pragma unroll
+            for (int k = s2 + 1; k <= H; ++k) {
+                const float de = iw[H + s2 - k] == cur ? d : 0.0f;
+                cn[H + s2 - k] = __builtin_fmaf(w[W - 1 - k], de, cn[H + s2 - k]);
+            }
+        }
+    }
+    finish(VPT - 1, acc[(VPT - 1) & 1], carry[(VPT - 1) & 1], cn, true);
+}
+
+// One (row, segment) item: the tile's loads go out first, then the halo,
+// weight and bias reads (scalar loads, issued together: the bias address is
+// always valid, so no branch holds them apart), which all complete before
+// the arithmetic starts -- the empty asm uses their values, so the compiler
+// can neither sink a load into the arithmetic nor wait for each on its own.
 template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
 __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c, int32_t t0,
                                               float* pw, float& pb) {
@@ -352,7 +541,8 @@ __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane
 #pragma unroll
     for (int k = 0; k < W; ++k) wq[k] = uniform_f32(-kLog2e * w[k]);
     const float bq = uniform_f32(-kLog2e * bias);
-    bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
+    if constexpr (SEQ) bwd_rows_compute_seq<T, W, VPT, SILU, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
+    else bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
 }
 
 // One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
