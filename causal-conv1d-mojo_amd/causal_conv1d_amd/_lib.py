@@ -17,7 +17,7 @@ from pathlib import Path
 _LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libcc1d_amd.so"
 ABI_VERSION = 3
 # fp32 elements of the static device scratch of cc1d_bwd_typed_noalloc (CC1D_NOALLOC_WORKSPACE_FLOATS)
-NOALLOC_WORKSPACE_FLOATS = 1 << 22
+NOALLOC_WORKSPACE_FLOATS = 1 << 21
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32

@@ -65,8 +65,10 @@ enum cc1d_status {
                                        CC1D_NOALLOC_WORKSPACE_FLOATS floats of workspace */
 };
 
-/* Size (fp32 elements) of the static device scratch of cc1d_bwd_typed_noalloc: 16 MiB per GPU. */
-#define CC1D_NOALLOC_WORKSPACE_FLOATS ((int64_t)1 << 22)
+/* Size (fp32 elements) of the static device scratch of cc1d_bwd_typed_noalloc: 8 MiB, reserved on
+   every GPU where the library's kernels are loaded, whether or not cc1d_bwd_typed_noalloc is called
+   (the largest benchmark need, 8 x 2048 x 16384 fp32 at width 4, is 1,310,720 floats). */
+#define CC1D_NOALLOC_WORKSPACE_FLOATS ((int64_t)1 << 21)
 
 /*
  * Forward: out[b,c,t] = act(bias[c] + sum_k weight[c,k] * xx(b,c,t+k-(W-1)))

@@ -195,3 +195,28 @@ def test_varlen_validation_codes(lib):
     assert call(state_len=-1) == ERR_SHAPE
     assert call() == ERR_NULL
     assert call(batch=0) == OK
+
+
+def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4):
+    p = _lib.BwdParams()
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the size is computed on the host
+    p.x = p.weight = p.dout = p.dx = fake
+    p.batch, p.dim, p.seqlen, p.width = B, D, L, W
+    strides = (D * L, 1, D) if channel_last else (D * L, L, 1)
+    p.x_stride[:] = p.dout_stride[:] = p.dx_stride[:] = strides
+    p.weight_stride[:] = (W, 1)
+    p.dtype, p.apply_silu = dtype, 1
+    return lib.cc1d_bwd_workspace_floats(ctypes.byref(p))
+
+
+def test_workspace_sizes_of_the_benchmark_configurations(lib):
+    """The typed backward's workspace at the benchmark configurations (the figures INTEGRATION.md
+    quotes), every one within the allocation-free entry point's static scratch."""
+    sizes = {
+        "C2": _workspace_floats(lib, 4, 5120, 2048, 1),
+        "C3": _workspace_floats(lib, 1, 4096, 8192, 1, channel_last=True),
+        "C5 bf16": _workspace_floats(lib, 8, 2048, 16384, 1),
+        "C5 fp32": _workspace_floats(lib, 8, 2048, 16384, 2),
+    }
+    assert sizes == {"C2": 102_400, "C3": 163_840, "C5 bf16": 655_360, "C5 fp32": 1_310_720}
+    assert max(sizes.values()) <= _lib.NOALLOC_WORKSPACE_FLOATS == 2_097_152

@@ -55,11 +55,12 @@ def _run(fn, prob):
     return dx, dw, db, di
 
 
-# (case, first problem (B, D, L), second, smaller problem, dtype); the channel-last first
-# problem is the C3 shape, whose workspace (2.6 M floats) is the largest of the benchmark
-# configurations
+# (case, first problem (B, D, L), second, smaller problem, dtype); the first rows_c5 problem
+# is benchmark configuration C5 in fp32, whose workspace (1,310,720 floats at width 4) is the
+# largest of the benchmark configurations; the channel-last one is C3 (163,840 floats)
 CASES = [
     ("rows", (4, 512, 2048), (2, 96, 700), torch.bfloat16),
+    ("rows_c5", (8, 2048, 16384), (2, 96, 700), torch.float32),
     ("channel_last", (1, 4096, 8192), (3, 130, 515), torch.bfloat16),
     ("seq_idx", (2, 256, 4096), (2, 64, 333), torch.float16),
     ("states", (3, 192, 1000), (1, 40, 2), torch.float32),
