@@ -20,7 +20,7 @@ import pytest
 import torch
 
 import causal_conv1d_amd as cc
-from causal_conv1d_amd import _fn, _update, reference
+from causal_conv1d_amd import reference
 
 
 def test_public_names_and_version():
