@@ -83,10 +83,10 @@ __device__ __forceinline__ void bwd_rows_load(const cc1d_bwd_params& p, int lane
     r.gn = tn < L ? gq : vzero();
 }
 
-// One wavefront-segment of row (b, c) from its loaded tile: writes dx (and
-// dinitial_states) and adds this segment's weight/bias-gradient partials
-// into pw / pb.
-template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+// One wavefront-segment of row (b, c) from its loaded tile, without seq_idx
+// (bwd_rows_compute_seq below has it): writes dx (and dinitial_states) and
+// adds this segment's weight/bias-gradient partials into pw / pb.
+template <typename T, int W, int VPT, bool SILU, bool FULL>
 __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
                                                  int32_t t0, const RowTile<VPT>& r, const float* w, const float* wq,
                                                  float bq, float* pw, float& pb) {
@@ -101,28 +101,6 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         const auto& v = r.v;
         const auto& gv = r.gv;
         const u32x4 h = r.h, xn = r.xn, gn = r.gn;
-
-        int32_t id[VPT][EPV];
-        int32_t hid[H], nid[H];
-        if constexpr (SEQ) {
-            const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
-#pragma unroll
-            for (int j = 0; j < VPT; ++j) {
-                const int32_t t = t0 + (j * 64 + lane) * EPV;
-#pragma unroll
-                for (int q = 0; q < EPV / 4; ++q) {
-                    const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
-                                            : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < H; ++i) {
-                hid[i] = (lane == 0 && t0 - H + i >= 0) ? sr[t0 - H + i] : -1;
-                nid[i] = (lane == 63 && tn + i < L) ? sr[tn + i] : -1;
-            }
-        }
 
         const bool init_row = p.initial_states != nullptr && t0 == 0;  // wave-uniform
         const bool use_init = init_row && lane == 0;
@@ -170,18 +148,6 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
             for (int i = 0; i < H; ++i) win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
 #pragma unroll
             for (int i = 0; i < EPV; ++i) win[H + i] = vget<T>(v[j], i);
-            int32_t sw[H + EPV];
-            if constexpr (SEQ) {
-#pragma unroll
-                for (int i = 0; i < H; ++i) {
-                    const int32_t send = (lane == 63) ? (j > 0 ? id[j > 0 ? j - 1 : 0][EPV - H + i] : -1)
-                                                      : id[j][EPV - H + i];
-                    const int32_t r = lane_get(send, prev_lane);
-                    sw[i] = (j == 0 && lane == 0) ? hid[i] : r;
-                }
-#pragma unroll
-                for (int i = 0; i < EPV; ++i) sw[H + i] = id[j][i];
-            }
 #pragma unroll
             for (int i = 0; i < EPV; ++i) {
                 const float g = vget<T>(gv[j], i);
@@ -190,29 +156,14 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                     // q = -log2(e) * pre, from pre-scaled weights and bias
                     float q = bq;
 #pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if constexpr (SEQ) {
-                            if (sw[i + k] == sw[H + i]) q = __builtin_fmaf(wq[k], win[i + k], q);
-                        } else {
-                            q = __builtin_fmaf(wq[k], win[i + k], q);
-                        }
-                    }
+                    for (int k = 0; k < W; ++k) q = __builtin_fmaf(wq[k], win[i + k], q);
                     d = silu_bwd_q(g, q);
                 }
                 if (!FULL && t >= L) d = 0.0f;
-                if constexpr (SEQ) {
-                    if (sw[H + i] < 0) d = 0.0f;
-                }
                 dpj[i] = d;
                 pb += d;
 #pragma unroll
-                for (int k = 0; k < W; ++k) {
-                    if constexpr (SEQ) {
-                        if (sw[i + k] == sw[H + i]) pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
-                    } else {
-                        pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
-                    }
-                }
+                for (int k = 0; k < W; ++k) pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
             }
         };
 
@@ -222,35 +173,20 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
             const int32_t t = t0 + (j * 64 + lane) * EPV;
             const bool lastv = j == VPT - 1;
             float de[EPV + H];
-            int32_t ie[EPV + H];
 #pragma unroll
-            for (int i = 0; i < EPV; ++i) {
-                de[i] = dpj[i];
-                if constexpr (SEQ) ie[i] = id[j][i];
-            }
+            for (int i = 0; i < EPV; ++i) de[i] = dpj[i];
 #pragma unroll
             for (int i = 0; i < H; ++i) {
                 const float send = (lane == 0) ? (lastv ? 0.0f : dpn[i]) : dpj[i];
                 const float r = lane_get(send, next_lane);
                 de[EPV + i] = (lane == 63 && lastv) ? dpn[i] : r;
-                if constexpr (SEQ) {
-                    const int32_t s = (lane == 0) ? (j + 1 < VPT ? id[j + 1 < VPT ? j + 1 : 0][i] : -1) : id[j][i];
-                    const int32_t ri = lane_get(s, next_lane);
-                    ie[EPV + i] = (lane == 63 && lastv) ? nid[i] : ri;
-                }
             }
             float o[EPV];
 #pragma unroll
             for (int i = 0; i < EPV; ++i) {
                 float acc = 0.0f;
 #pragma unroll
-                for (int k = 0; k < W; ++k) {
-                    if constexpr (SEQ) {
-                        if (ie[i + k] == ie[i]) acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
-                    } else {
-                        acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
-                    }
-                }
+                for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
                 o[i] = acc;
             }
             // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
@@ -294,15 +230,10 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         for (int i = 0; i < H; ++i) dn[i] = 0.0f;
         if (tn < L) {
             float xw[2 * H];
-            int32_t iw[2 * H];
 #pragma unroll
             for (int i = 0; i < H; ++i) {
                 xw[i] = vget<T>(v[VPT - 1], EPV - H + i);
                 xw[H + i] = vget<T>(xn, i);
-                if constexpr (SEQ) {
-                    iw[i] = id[VPT - 1][EPV - H + i];
-                    iw[H + i] = nid[i];
-                }
             }
 #pragma unroll
             for (int i = 0; i < H; ++i) {
@@ -311,19 +242,10 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                 if constexpr (SILU) {
                     float q = bq;
 #pragma unroll
-                    for (int k = 0; k < W; ++k) {
-                        if constexpr (SEQ) {
-                            if (iw[i + k] == iw[H + i]) q = __builtin_fmaf(wq[k], xw[i + k], q);
-                        } else {
-                            q = __builtin_fmaf(wq[k], xw[i + k], q);
-                        }
-                    }
+                    for (int k = 0; k < W; ++k) q = __builtin_fmaf(wq[k], xw[i + k], q);
                     d = silu_bwd_q(g, q);
                 }
                 if (tn + i >= L) d = 0.0f;
-                if constexpr (SEQ) {
-                    if (iw[H + i] < 0) d = 0.0f;
-                }
                 dn[i] = d;
             }
         }
@@ -542,7 +464,7 @@ __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane
     for (int k = 0; k < W; ++k) wq[k] = uniform_f32(-kLog2e * w[k]);
     const float bq = uniform_f32(-kLog2e * bias);
     if constexpr (SEQ) bwd_rows_compute_seq<T, W, VPT, SILU, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
-    else bwd_rows_compute<T, W, VPT, SILU, SEQ, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
+    else bwd_rows_compute<T, W, VPT, SILU, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
 }
 
 // One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
