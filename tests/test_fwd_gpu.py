@@ -240,3 +240,25 @@ def test_torch_compile_autograd():
 
     f(x, w, b).backward()
     assert x.grad.shape == x.shape and w.grad.shape == w.shape and b.grad.shape == b.shape
+
+
+def test_launch_status_ignores_an_earlier_unrelated_error():
+    """A kernel launch reports its own status: an error that an unrelated HIP call left pending on
+    the thread (here an invalid device number) is not returned as the library's failure."""
+    import ctypes
+    import os
+
+    from causal_conv1d_amd._native import native_fwd
+
+    hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)  # the runtime torch and the library share
+    hip.hipSetDevice.argtypes = [ctypes.c_int]
+    x, w, b, _ = make_inputs(2, 64, 512, 4, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty_like(x)
+    torch.cuda.synchronize()
+    try:
+        assert hip.hipSetDevice(-1) != 0  # refused: leaves an error on the thread, touches no GPU state
+        native_fwd(x, w, b, None, None, out, True)  # raises if cc1d_fwd returns a status other than OK
+    finally:
+        hip.hipGetLastError()  # take the planted error off the thread before torch checks it
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.causal_conv1d_fn(x.cpu(), w.cpu(), b.cpu(), activation="silu"), torch.bfloat16)
