@@ -146,6 +146,24 @@ def test_seq_idx_backward_segments(dtype, seqlen):
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("width", [2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("pattern", ["repeat_ids", "with_padding"])
+def test_seq_idx_backward_widths_across_lanes_and_segments(dtype, width, pattern):
+    """The seq_idx row backward scatters dx across lanes, vectors and segments (a carry per
+    lane boundary, the next segment's first W-1 positions recomputed): every width, a row of
+    3 segments (the last one partial), ids that reappear inside a window or are padded."""
+    if dtype == torch.float32 and width > 5:
+        pytest.skip("fp32 widths above 5 are rejected by the API (reference _fn.py:405-414)")
+    L = 4096 + 2 * 128 + 8  # bf16/fp16: 3 segments of up to 2048; fp32: 5 of up to 1024
+    x, w, b, _ = make_inputs(2, 6, L, width, dtype=dtype)
+    dout = make_inputs(2, 6, L, width, dtype=dtype, seed=1)[0]
+    s = seq_pattern(pattern, 2, L)
+    got = _gpu_grads(x, w, b, dout, seq_idx=s, activation="silu")
+    _check(got, O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu"), dtype,
+           scales(x, w, b, dout, seq_idx=s, activation="silu"))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("layout", ["channel_last", "channel_slice", "sliced_seq"])
 def test_backward_strided(dtype, layout):
     B, D, L, W = 2, 64, 128, 4
