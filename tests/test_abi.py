@@ -210,8 +210,8 @@ def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4):
 
 
 def test_workspace_sizes_of_the_benchmark_configurations(lib):
-    """The typed backward's workspace at the benchmark configurations (the figures INTEGRATION.md
-    quotes), every one within the allocation-free entry point's static scratch."""
+    """The typed backward's workspace at the benchmark configurations, every one within the
+    allocation-free entry point's static scratch."""
     sizes = {
         "C2": _workspace_floats(lib, 4, 5120, 2048, 1),
         "C3": _workspace_floats(lib, 1, 4096, 8192, 1, channel_last=True),
