@@ -145,6 +145,53 @@ def test_seq_idx_backward_segments(dtype, seqlen):
            scales(x, w, b, dout, seq_idx=s, activation="silu"))
 
 
+_NONFINITE_VIEWS = {
+    "rows": None,
+    "channel_last": lambda t: t.transpose(1, 2).contiguous().transpose(1, 2),
+    "strided": lambda t: torch.stack([t, t], -1)[..., 0],
+}
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("layout", list(_NONFINITE_VIEWS))
+def test_seq_idx_nonfinite_padding_follows_the_reference(dtype, layout):
+    """Padding positions (negative ids) holding NaN / inf in x and dout. dpre there is zero
+    whatever they hold (bwd_full_cpu/kernel.mojo:75-77), so the output, dx and dbias stay
+    finite; the weight gradient adds 0 * x over a padding run's kept taps (kernel.mojo:264-274),
+    which is NaN exactly where such an x is not finite, as in the reference. The finite
+    entries are compared as usual."""
+    B, D, L, W = 2, 16, 1024, 4
+    x, w, b, _ = make_inputs(B, D, L, W, dtype=dtype)
+    dout = make_inputs(B, D, L, W, dtype=dtype, seed=1)[0]
+    s = seq_pattern("with_padding", B, L).clone()  # positions 16..31 padded (-1)
+    s[:, 600:610] = -3                               # a second run, another negative id
+    pad = s[0] < 0
+    clean_x, clean_g = x.clone(), dout.clone()
+    clean_x[:, :, pad] = 0
+    clean_g[:, :, pad] = 0
+    x[:, : D // 2, 16:32] = float("nan")             # channels 0..7: NaN through the first run
+    x[:, D // 2 : 3 * D // 4, 603] = float("inf")    # channels 8..11: one inf in the second
+    dout[:, :, pad] = float("nan")                   # every channel: NaN dout at padding
+    xg = x.to(DEV).requires_grad_()
+    wg = w.to(DEV).requires_grad_()
+    bg = b.to(DEV).requires_grad_()
+    view = _NONFINITE_VIEWS[layout]
+    out = cc.causal_conv1d_fn(xg if view is None else view(xg), wg, bg, seq_idx=s.to(DEV), activation="silu")
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    rout = O.causal_conv1d_fn(x, w, b, seq_idx=s, activation="silu")
+    rdx, rdw, rdb, _ = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, activation="silu")
+    assert_close(out.detach().cpu(), rout, dtype, name="out")
+    assert_close(xg.grad.cpu(), rdx, dtype, name="dx")
+    sw, sb = scales(clean_x, w, b, clean_g, seq_idx=s, activation="silu")
+    assert_reduction_close(bg.grad.cpu(), rdb, dtype, scale=sb, name="dbias")
+    dw = wg.grad.cpu()
+    bad = ~torch.isfinite(rdw.double())
+    assert bad[: 3 * D // 4].all() and not bad[3 * D // 4 :].any()  # the case is what it says
+    assert torch.equal(torch.isnan(dw), bad), "dweight: non-finite entries differ from the reference's"
+    assert_reduction_close(dw[~bad], rdw[~bad], dtype, scale=sw[~bad], name="dweight")
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("width", [2, 3, 4, 5, 6, 7, 8, 9])
 @pytest.mark.parametrize("pattern", ["repeat_ids", "with_padding"])
