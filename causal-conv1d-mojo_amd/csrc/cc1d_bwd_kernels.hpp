@@ -633,12 +633,16 @@ __device__ __forceinline__ void bwd_chunk(const cc1d_bwd_params& p, int64_t b, i
 // is 32-bit inside a batch (the launcher checks the ranges).
 //
 // Launch shape (C3, 8192 x 4096 bf16): chunks of 4 steps, runs of 128, 8
-// runs per block -- 2048 wavefronts, two per SIMD. Measured against it
-// (same box, us for seq_idx / initial_states): tiles of 16 steps loaded at
-// once, 4 per block, 46.3 / 45.0 (the previous kernel); runs of 64 or 96
-// steps 48-49; runs of 192 52-57; chunks of 8 steps 46-48; 4 runs per block
-// 44.0 / 42.0; 8 runs per block 42.1 / 41.0. A copy with the same access
-// pattern and no arithmetic takes 36.8 us.
+// runs per block -- 2048 wavefronts, two per SIMD: 39.1-39.7 / 37.9-38.2 us
+// (seq_idx / initial_states); the same access pattern with no arithmetic
+// takes 34.1-34.4 us. Measured against it in the same sessions: runs of 64
+// steps (8 or 16 per block) 46.0 / 42.0 us and of 96 54.9 us for seq_idx;
+// three chunks in flight instead of one 43.1 / 42.0; the block order
+// remapped to XCDs 41.4-41.7 for seq_idx; four wavefronts sharing each
+// chunk's 1 KB row pieces through LDS (16 bytes per lane, a barrier per
+// chunk) 41.7 / 40.3 at best; and, with no arithmetic, 8-byte lanes no
+// faster than these 4-byte ones (34.4 us). The earlier tile kernel (16
+// steps loaded at once, 4 per block) took 46.3 / 45.0.
 
 // The weights and bias of a lane's channels, kept raw: they are read before
 // the walk and converted where they are used, so no conversion waits for
