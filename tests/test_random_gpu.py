@@ -13,10 +13,14 @@ shapes that no hand-written case picks. A second sweep does the same for the
 decode update (widths 2..9 for every dtype there): linear or circular buffers,
 with and without a state pool; a third gathers varlen states from random
 packings (empty sequences included). The case's parameters are in its id.
+A "large" class adds rows of several segments, whole channel-last channel
+groups and sequences of 1000-5000 steps. CC1D_RANDOM_SCALE=N multiplies every
+sweep's case count (new seeds, same distributions).
 """
 
 from __future__ import annotations
 
+import os
 import random
 
 import pytest
@@ -57,7 +61,24 @@ def _fn_id(c):
             f"-{'bias' if c['bias'] else 'nobias'}-{c['act']}{'-wT' if c['wt'] else ''}{'-doutcl' if c['dcl'] else ''}")
 
 
-FN_CASES = [_fn_case(s) for s in range(360)]
+SCALE = int(os.environ.get("CC1D_RANDOM_SCALE", "1"))
+
+
+def _fn_large_case(seed):
+    """The same draws with a large shape: several row segments, whole channel-last groups."""
+    r = random.Random(7_000_000 + seed)
+    c = _fn_case(seed)
+    c.update(
+        B=r.randint(1, 2),
+        D=r.choice([128 * r.randint(1, 8), 512 * r.randint(1, 2), r.randint(300, 700)]),
+        L=r.choice([2048 * r.randint(1, 2), r.randint(2000, 5000), 1024 * r.randint(1, 4) + r.choice([0, 8, 264])]),
+        W=r.randint(2, 5 if c["dt"] == "fp32" else 9),
+        layout=r.choice(["contig", "cl", "cl", "sliced"]),
+    )
+    return c
+
+
+FN_CASES = [_fn_case(s) for s in range(360 * SCALE)] + [_fn_large_case(s) for s in range(24 * SCALE)]
 
 
 def _rand(g, *shape, dtype):
@@ -171,7 +192,7 @@ def _upd_id(c):
             f"-{'bias' if c['bias'] else 'nobias'}-{c['act']}{'-2d' if c['two_d'] else ''}")
 
 
-UPD_CASES = [_upd_case(s) for s in range(150)]
+UPD_CASES = [_upd_case(s) for s in range(150 * SCALE)]
 
 
 @pytest.mark.parametrize("c", UPD_CASES, ids=_upd_id)
@@ -207,7 +228,7 @@ def _varlen_case(seed):
                 S=r.randint(0, 12), dt=r.choice(list(DT)), maxlen=r.choice([3, 20, 300]), strided=r.random() < 0.3)
 
 
-VARLEN_CASES = [_varlen_case(s) for s in range(60)]
+VARLEN_CASES = [_varlen_case(s) for s in range(60 * SCALE)]
 
 
 @pytest.mark.parametrize("c", VARLEN_CASES, ids=lambda c: (f"s{c['seed']}-{c['dt']}-n{c['n']}D{c['D']}S{c['S']}"
