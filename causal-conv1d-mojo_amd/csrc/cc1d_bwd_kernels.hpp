@@ -21,7 +21,11 @@
 //
 // Kernels
 //   bwd_rows_vec -- channel-first rows, same lane layout and item order as
-//                   fwd_rows_vec (one item per wavefront, 4 per block).
+//                   fwd_rows_vec (one item per wavefront, 4 per block),
+//                   ragged rows included: positions count from the 16-byte
+//                   boundary at or before the row's first element (the row is
+//                   [m, m + L)), dpre is zero outside the row, and the vectors
+//                   shared with neighbouring rows are stored element by element.
 //   bwd_clw      -- channel-last (unit channel stride); a lane owns 4 bytes of
 //                   adjacent channels, a wavefront walks a run of time steps.
 //   bwd_generic  -- any strides; one thread per (b, c, chunk of time).
@@ -40,6 +44,7 @@ struct BwdArgs {
     int64_t n_items;  // rows_vec: (row, segment) items; generic: threads
     int64_t chunk;    // cl: time steps per run; generic: time steps per thread
     int64_t groups;   // cl: channel groups of 64 * CPL
+    int32_t ragged;   // rows_vec: rows may start off a 16-byte boundary / end inside a vector (kernel variant)
 };
 
 // channel-first rows: (row, segment) items per block, one per wavefront
@@ -61,13 +66,13 @@ template <int VPT> struct RowTile {
 // inside the row.
 template <typename T, int VPT, bool FULL>
 __device__ __forceinline__ void bwd_rows_load(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c, int32_t t0,
-                                              RowTile<VPT>& r) {
+                                              int32_t m, RowTile<VPT>& r) {
     constexpr int EPV = elems16<T>::value;
     constexpr int SEG = 64 * VPT * EPV;
-    const int32_t L = (int32_t)p.seqlen;
+    const int32_t L = (int32_t)p.seqlen + m;  // the row's end (its start is m)
     const int32_t tn = t0 + SEG;  // first position of the next segment
-    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
-    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1];
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1] - m;
+    const T* __restrict__ gr = static_cast<const T*>(p.dout) + b * p.dout_stride[0] + c * p.dout_stride[1] - m;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int32_t t = t0 + (j * 64 + lane) * EPV;
@@ -85,22 +90,20 @@ __device__ __forceinline__ void bwd_rows_load(const cc1d_bwd_params& p, int lane
 
 // One wavefront-segment of row (b, c) from its loaded tile, without seq_idx
 // (bwd_rows_compute_seq below has it): writes dx (and dinitial_states) and
-// adds this segment's weight/bias-gradient partials into pw / pb.
-template <typename T, int W, int VPT, bool SILU, bool FULL>
+// adds this segment's weight/bias-gradient partials into pw / pb. RAG: the
+// row starts m elements past a 16-byte boundary (m is 0 otherwise).
+template <typename T, int W, int VPT, bool SILU, bool FULL, bool RAG>
 __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0, const RowTile<VPT>& r, const float* w, const float* wq,
-                                                 float bq, float* pw, float& pb) {
+                                                 int32_t t0, int32_t m, RowTile<VPT> r, const float* w,
+                                                 const float* wq, float bq, float* pw, float& pb) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int SEG = 64 * VPT * EPV;
     static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
-    const int32_t L = (int32_t)p.seqlen;
+    const int32_t L = (int32_t)p.seqlen + m;  // the row is [m, L) in this segment's positions
     {
         const int32_t tn = t0 + SEG;  // first position of the next segment
-        T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
-        const auto& v = r.v;
-        const auto& gv = r.gv;
-        const u32x4 h = r.h, xn = r.xn, gn = r.gn;
+        T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1] - m;
 
         const bool init_row = p.initial_states != nullptr && t0 == 0;  // wave-uniform
         const bool use_init = init_row && lane == 0;
@@ -113,17 +116,35 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
 #pragma unroll
             for (int i = 0; i < H; ++i) hinit[i] = ld_uniform(is + i * p.initial_states_stride[2]);
         }
-        // dfinal_states of this row when the segment holds the row's end (wave-uniform)
+        // dfinal_states of this row when the segment holds one of the row's
+        // last W-1 positions (wave-uniform; a ragged row's may span two
+        // segments, an aligned row's lie in its last vector)
         float dfin[H];
 #pragma unroll
         for (int i = 0; i < H; ++i) dfin[i] = 0.0f;
-        const bool dfin_row = p.dfinal_states != nullptr && tn >= L;
+        const bool dfin_row = p.dfinal_states != nullptr && tn > L - H;
         if (dfin_row) {
             const T* dfs = static_cast<const T*>(p.dfinal_states) + b * p.dfinal_states_stride[0] +
                            c * p.dfinal_states_stride[1];
 #pragma unroll
             for (int i = 0; i < H; ++i) dfin[i] = ld_uniform(dfs + i * p.dfinal_states_stride[2]);
         }
+        // a ragged row's first vector holds m elements of the previous row:
+        // they are positions -m .. -1 of this one (x: initial_states or zero;
+        // dout: zero)
+        if (RAG && !FULL && t0 == 0 && m > 0 && lane == 0) {
+            float fx[EPV], fg[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                fx[e] = e >= m ? vget<T>(r.v[0], e) : pick<H>(hinit, e - m + H);
+                fg[e] = e >= m ? vget<T>(r.gv[0], e) : 0.0f;
+            }
+            r.v[0] = vpack<T>(fx);
+            r.gv[0] = vpack<T>(fg);
+        }
+        const auto& v = r.v;
+        const auto& gv = r.gv;
+        const u32x4 h = r.h, xn = r.xn, gn = r.gn;
 
         // The vectors are processed in order: dpre of vector j (with its
         // gradient partials), then dx of vector j - 1, which needs dpre of
@@ -143,9 +164,18 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                 pv[d] = lane_get(send, prev_lane);
             }
             if (j == 0 && lane == 0) pv = h;
+            // an aligned row's first vector past its end: its window reads
+            // zero too, so that no x of the row meets that vector's zero dpre
+            // (zero times a non-finite x would be NaN)
+            if (!FULL && !RAG && t >= L) pv = vzero();
             float win[H + EPV];
 #pragma unroll
-            for (int i = 0; i < H; ++i) win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
+            for (int i = 0; i < H; ++i) {
+                if constexpr (FULL || !RAG)  // m == 0 whenever a first segment is full
+                    win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
+                else  // before the row: position i - H - m, initial_states slot i - m
+                    win[i] = (j == 0 && use_init) ? pick<H>(hinit, i - m) : vget<T>(pv, EPV - H + i);
+            }
 #pragma unroll
             for (int i = 0; i < EPV; ++i) win[H + i] = vget<T>(v[j], i);
 #pragma unroll
@@ -159,11 +189,19 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                     for (int k = 0; k < W; ++k) q = __builtin_fmaf(wq[k], win[i + k], q);
                     d = silu_bwd_q(g, q);
                 }
-                if (!FULL && t >= L) d = 0.0f;
+                // outside the row: dpre is zero and the position adds nothing
+                // to the weight gradient (a select, not a product with zero,
+                // which a non-finite x there would turn into NaN). Aligned
+                // rows end on a vector boundary: the test is the vector's.
+                const bool outside = !FULL && (RAG ? (t + i < m || t + i >= L) : t >= L);
+                if (outside) d = 0.0f;
                 dpj[i] = d;
                 pb += d;
 #pragma unroll
-                for (int k = 0; k < W; ++k) pw[k] = __builtin_fmaf(d, win[i + k], pw[k]);
+                for (int k = 0; k < W; ++k) {
+                    const float s = __builtin_fmaf(d, win[i + k], pw[k]);
+                    pw[k] = (RAG && outside) ? pw[k] : s;
+                }
             }
         };
 
@@ -189,35 +227,68 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                 for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[W - 1 - k], de[i + k], acc);
                 o[i] = acc;
             }
-            // dfinal_states tail (_fn.py:308-315): L % EPV == 0 and L >= EPV >= H
-            // here, so the W-1 tail positions are the end of the last vector.
-            // A wave-uniform branch skips it for every segment without the row
-            // end (as a lane-masked block it was issued, empty, by all of them).
+            // dfinal_states tail (_fn.py:308-315): the row's last W-1
+            // positions [L - H, L), those inside the row. A wave-uniform
+            // branch skips it for every segment without the row end (as a
+            // lane-masked block it was issued, empty, by all of them).
             if (dfin_row) {
-                const bool last = t + EPV == L;
+                if constexpr (!RAG) {  // the row's last vector ends with them
+                    const bool last = t + EPV == L;
 #pragma unroll
-                for (int i = EPV - H; i < EPV; ++i) {
-                    const float v = round_to<T>(o[i]) + dfin[H - EPV + i];
-                    o[i] = last ? v : o[i];
+                    for (int i = EPV - H; i < EPV; ++i) {
+                        const float v = round_to<T>(o[i]) + dfin[H - EPV + i];
+                        o[i] = last ? v : o[i];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < EPV; ++i) {
+                        const int32_t pos = t + i;
+                        const float v = round_to<T>(o[i]) + pick<H>(dfin, pos - L + H);
+                        o[i] = (pos >= L - H && pos < L && pos >= m) ? v : o[i];
+                    }
                 }
             }
-            if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
+            if constexpr (!RAG) {
+                if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
+            } else if (FULL || (t >= m && t + EPV <= L)) {
+                vstore_nt(dxr + t, vpack<T>(o));
+            } else if (t < L) {  // a vector shared with a neighbouring row
+#pragma unroll
+                for (int e = 0; e < EPV; ++e)
+                    if (t + e >= m && t + e < L) st(dxr, t + e, o[e]);
+            }
         };
 
         float dp[2][EPV];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             dpre_vec(j, dp[j & 1]);
-            if (j == 0 && p.dinitial_states != nullptr && t0 == 0 && lane == 0) {
-                // dinitial_states (bwd_full_cpu/kernel.mojo:210-219)
-                T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
-                        c * p.dinitial_states_stride[1];
+            if (j == 0 && p.dinitial_states != nullptr && t0 == 0) {  // wave-uniform
+                // dinitial_states (bwd_full_cpu/kernel.mojo:210-219) from dpre of
+                // positions 0 .. H-1: elements m .. m+H-1 of lane 0's first
+                // vector, the ones past its end in lane 1's
+                float d0[H];
 #pragma unroll
-                for (int i = 0; i < H; ++i) {
-                    float acc = 0.0f;
+                for (int q = 0; q < H; ++q) {
+                    if constexpr (FULL || !RAG) {
+                        d0[q] = dp[0][q];
+                    } else {
+                        const float own = pick<EPV>(dp[0], m + q);
+                        const float nxt = __int_as_float(
+                            __builtin_amdgcn_readlane(__float_as_int(pick<EPV>(dp[0], m + q - EPV)), 1));
+                        d0[q] = m + q < EPV ? own : nxt;
+                    }
+                }
+                if (lane == 0) {
+                    T* di = static_cast<T*>(p.dinitial_states) + b * p.dinitial_states_stride[0] +
+                            c * p.dinitial_states_stride[1];
 #pragma unroll
-                    for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], dp[0][i - k], acc);
-                    st(di, i * p.dinitial_states_stride[2], acc);
+                    for (int i = 0; i < H; ++i) {
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int k = 0; k <= i; ++k) acc = __builtin_fmaf(w[k], d0[i - k], acc);
+                        st(di, i * p.dinitial_states_stride[2], acc);
+                    }
                 }
             }
             if (j > 0) dx_vec(j - 1, dp[(j - 1) & 1], dp[j & 1]);
@@ -265,41 +336,66 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
 // carry that the owning lane fetches from its neighbour (lane 63: from lane
 // 0 of the next vector, or from the next segment's first H positions); each
 // dx sum is the gather's fma chain with that carry added as one term.
-template <typename T, int W, int VPT, bool SILU, bool FULL>
+template <typename T, int W, int VPT, bool SILU, bool FULL, bool RAG>
 __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c,
-                                                     int32_t t0, const RowTile<VPT>& r, const float* w,
-                                                     const float* wq, float bq, float* pw, float& pb) {
+                                                     int32_t t0, int32_t m, RowTile<VPT> r,
+                                                     const float* w, const float* wq, float bq, float* pw,
+                                                     float& pb) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     constexpr int SEG = 64 * VPT * EPV;
     static_assert(H <= EPV, "the halo must fit in one 16-byte vector");
     constexpr int D0 = ((EPV - H) * (int)sizeof(T)) / 4;
-    const int32_t L = (int32_t)p.seqlen;
+    const int32_t Lr = (int32_t)p.seqlen;  // the row's length
+    const int32_t L = Lr + m;              // its end: the row is [m, L) in these positions
     const int32_t tn = t0 + SEG;  // first position of the next segment
-    T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1];
+    T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1] - m;
     const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
+    // (unit time stride) ragged rows: a vector's ids start rid ids past a
+    // 16-byte boundary (its first position, t - m, is a multiple of 4 plus -m)
+    const int rid = RAG ? (int)uniform32(((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) - (uint32_t)m) & 3u) : 0;
     const int prev_lane = (lane + 63) & 63;
     const int next_lane = (lane + 1) & 63;
+    // a ragged row's first vector holds m elements of the previous row: x
+    // there reads as zero, as before an aligned row (a padding position's id
+    // matches theirs, -1, and a tap is kept by its id alone)
+    if (RAG && !FULL && t0 == 0 && m > 0 && lane == 0) {
+        float fx[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) fx[e] = e >= m ? vget<T>(r.v[0], e) : 0.0f;
+        r.v[0] = vpack<T>(fx);
+    }
 
-    // ids: the lane's positions (-1 past the row end), and the H before and
+    // ids: the lane's positions (-1 outside the row), and the H before and
     // after the segment (wave-uniform, -1 outside the row)
     int32_t id[VPT][EPV];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int32_t t = t0 + (j * 64 + lane) * EPV;
+        if constexpr (!RAG) {  // 16-byte vectors of 4 ids
 #pragma unroll
-        for (int q = 0; q < EPV / 4; ++q) {
-            const u32x4 sv = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
-                                             : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+            for (int q = 0; q < EPV / 4; ++q) {
+                const u32x4 sv = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                                                 : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) id[j][4 * q + e] = (int32_t)sv[e];
+                for (int e = 0; e < 4; ++e) id[j][4 * q + e] = (int32_t)sv[e];
+            }
+        } else if (FULL || (t >= m && t + EPV <= L)) {  // every position inside the row
+            load_i32_shifted<EPV>(sr + (t - m), rid, id[j]);
+        } else {  // one id per position; -1 outside the row
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const int32_t pos = t + e - m;
+                id[j][e] = (pos >= 0 && pos < Lr) ? sr[pos] : -1;
+            }
         }
     }
     int32_t hid[H], nid[H];
 #pragma unroll
     for (int i = 0; i < H; ++i) {
-        hid[i] = t0 - H + i >= 0 ? ld_uniform(sr + (t0 - H + i)) : -1;
-        nid[i] = tn + i < L ? ld_uniform(sr + (tn + i)) : -1;
+        const int32_t ph = t0 - H + i - m, pn = tn + i - m;  // row positions
+        hid[i] = ph >= 0 ? ld_uniform(sr + ph) : -1;
+        nid[i] = pn < Lr ? ld_uniform(sr + pn) : -1;
     }
 
     float acc[2][EPV];  // dx sums of the lane's positions, by vector parity
@@ -317,7 +413,15 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
             if (local && lane == 63) rv = nxt[i];
             a[EPV - H + i] += rv;
         }
-        if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(a));
+        if constexpr (!RAG) {
+            if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(a));
+        } else if (FULL || (t >= m && t + EPV <= L)) {
+            vstore_nt(dxr + t, vpack<T>(a));
+        } else if (t < L) {  // a vector shared with a neighbouring row
+#pragma unroll
+            for (int e = 0; e < EPV; ++e)
+                if (t + e >= m && t + e < L) st(dxr, t + e, a[e]);
+        }
     };
 
 #pragma unroll
@@ -373,11 +477,15 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
                 for (int kk = 0; kk < W; ++kk) q = __builtin_fmaf(wq[kk], xe[kk], q);
                 d = silu_bwd_q(g, q);
             }
-            if (!FULL && t + e >= L) d = 0.0f;
-            if (cur < 0) d = 0.0f;
+            // outside the row: nothing added (a select, as in bwd_rows_compute)
+            const bool outside = !FULL && (RAG ? (t + e < m || t + e >= L) : t + e >= L);
+            if (outside || cur < 0) d = 0.0f;
             pb += d;
 #pragma unroll
-            for (int kk = 0; kk < W; ++kk) pw[kk] = __builtin_fmaf(d, xe[kk], pw[kk]);
+            for (int kk = 0; kk < W; ++kk) {
+                const float s = __builtin_fmaf(d, xe[kk], pw[kk]);
+                pw[kk] = outside ? pw[kk] : s;
+            }
             // dx[s - k] += w[W-1-k] * dpre[s] where tap W-1-k of s is kept
 #pragma unroll
             for (int k = 0; k <= H; ++k) {
@@ -442,11 +550,11 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
 // always valid, so no branch holds them apart), which all complete before
 // the arithmetic starts -- the empty asm uses their values, so the compiler
 // can neither sink a load into the arithmetic nor wait for each on its own.
-template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL, bool RAG>
 __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane, int64_t b, int64_t c, int32_t t0,
-                                              float* pw, float& pb) {
+                                              int32_t m, float* pw, float& pb) {
     RowTile<VPT> r;
-    bwd_rows_load<T, VPT, FULL>(p, lane, b, c, t0, r);
+    bwd_rows_load<T, VPT, FULL>(p, lane, b, c, t0, m, r);
     float w[W];
     const T* __restrict__ wr = static_cast<const T*>(p.weight) + c * p.weight_stride[0];
 #pragma unroll
@@ -463,8 +571,8 @@ __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane
 #pragma unroll
     for (int k = 0; k < W; ++k) wq[k] = uniform_f32(-kLog2e * w[k]);
     const float bq = uniform_f32(-kLog2e * bias);
-    if constexpr (SEQ) bwd_rows_compute_seq<T, W, VPT, SILU, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
-    else bwd_rows_compute<T, W, VPT, SILU, FULL>(p, lane, b, c, t0, r, w, wq, bq, pw, pb);
+    if constexpr (SEQ) bwd_rows_compute_seq<T, W, VPT, SILU, FULL, RAG>(p, lane, b, c, t0, m, r, w, wq, bq, pw, pb);
+    else bwd_rows_compute<T, W, VPT, SILU, FULL, RAG>(p, lane, b, c, t0, m, r, w, wq, bq, pw, pb);
 }
 
 // One (row, segment) item per wavefront, kRowsWPB per block; item = (row,
@@ -477,7 +585,7 @@ __device__ __forceinline__ void bwd_rows_item(const cc1d_bwd_params& p, int lane
 // in LDS and written in the dtype, so the typed backward needs no second
 // launch -- measured 2 us slower at C2: the block's rows lie in B regions
 // of the tensors instead of one.)
-template <typename T, int W, int VPT, bool SILU, bool SEQ>
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool RAG>
 __global__ void __launch_bounds__(64 * kRowsWPB) bwd_rows_vec(const BwdArgs a) {
     constexpr int SEG = 64 * VPT * elems16<T>::value;
     const cc1d_bwd_params& p = a.p;
@@ -494,10 +602,20 @@ __global__ void __launch_bounds__(64 * kRowsWPB) bwd_rows_vec(const BwdArgs a) {
 #pragma unroll
     for (int k = 0; k < W; ++k) pw[k] = 0.0f;
     float pb = 0.0f;
-    if (t0 + SEG <= (int32_t)p.seqlen)
-        bwd_rows_item<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0, pw, pb);
-    else
-        bwd_rows_item<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0, pw, pb);
+    constexpr int EPV = elems16<T>::value;
+    // ragged rows: the row starts m elements past a 16-byte boundary
+    int32_t m = 0;
+    if constexpr (RAG) {
+        const T* xrow = static_cast<const T*>(p.x) + (int64_t)b * p.x_stride[0] + (int64_t)c * p.x_stride[1];
+        m = (int32_t)uniform32((uint32_t)(reinterpret_cast<uintptr_t>(xrow) / sizeof(T)) & (EPV - 1));
+    }
+    const int32_t Lv = (int32_t)p.seqlen + m;
+    // a ragged row's last segment may lie past its end: it adds nothing but
+    // still writes its (zero) record
+    if ((t0 > 0 || m == 0) && t0 + SEG <= Lv)
+        bwd_rows_item<T, W, VPT, SILU, SEQ, true, RAG>(p, lane, b, c, t0, m, pw, pb);
+    else if (!RAG || t0 < Lv)
+        bwd_rows_item<T, W, VPT, SILU, SEQ, false, RAG>(p, lane, b, c, t0, m, pw, pb);
 
     // ---- weight / bias gradient: wavefront sum, then lanes 0..W add ----
     float mine = wave_sum(pb);
@@ -1122,6 +1240,29 @@ bool rows_vec_ok(const cc1d_bwd_params& p) {
     return true;
 }
 
+// ragged rows (a seqlen that is not a multiple of the vector, or rows that do
+// not start on a 16-byte boundary): unit time stride, and dout and dx laid out
+// like x modulo the vector -- the same element strides modulo EPV and bases a
+// multiple of 16 bytes apart -- so every row of each starts as far past a
+// 16-byte boundary as its row of x; seq_idx with a unit time stride
+template <typename T>
+bool rows_ragged_ok(const cc1d_bwd_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    if (p.width - 1 > EPV) return false;
+    if (p.x_stride[2] != 1 || p.dout_stride[2] != 1 || p.dx_stride[2] != 1) return false;
+    for (const int64_t* s : {p.dout_stride, p.dx_stride})
+        if ((s[0] - p.x_stride[0]) % EPV != 0 || (s[1] - p.x_stride[1]) % EPV != 0) return false;
+    const intptr_t x = reinterpret_cast<intptr_t>(p.x);
+    if ((reinterpret_cast<intptr_t>(p.dout) - x) % 16 != 0 || (reinterpret_cast<intptr_t>(p.dx) - x) % 16 != 0)
+        return false;
+    if (p.seq_idx != nullptr && (p.seq_idx_stride[1] != 1 || reinterpret_cast<uintptr_t>(p.seq_idx) % 4 != 0))
+        return false;
+    const int64_t lim = (int64_t)1 << 31;
+    if (p.seqlen + 64 * 4 * EPV + EPV >= lim) return false;
+    if (p.batch * p.dim * ceil_div(p.seqlen + EPV, 64 * EPV) >= lim) return false;
+    return true;
+}
+
 // channel-last tiles: unit channel stride, CPL | dim, rows aligned to the
 // CPL-channel lane vector, 32-bit positions inside a batch
 template <typename T, int CPL>
@@ -1179,11 +1320,17 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
     pl.vpt = 0;
     pl.cpl = 0;
     pl.rec_floats = W + 1;
-    if (W - 1 <= EPV && rows_vec_ok<T>(p)) {
-        const int64_t nvec = p.seqlen / EPV;
+    pl.a.ragged = 0;
+    const bool aligned = W - 1 <= EPV && rows_vec_ok<T>(p);
+    if (aligned || (W - 1 <= EPV && rows_ragged_ok<T>(p))) {
+        pl.a.ragged = aligned ? 0 : 1;
+        // vectors a row spans: a ragged row may start up to EPV - 1 elements
+        // past a vector boundary
+        const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
         const int64_t per = ceil_div(nvec, 64);
         pl.kind = kBwdRows;
-        pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+        // (the ragged kernels are built for 4 and 1 vectors per lane only)
+        pl.vpt = per >= 4 ? 4 : (per >= 2 && aligned ? 2 : 1);
         pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
         pl.a.n_items = p.batch * p.dim * pl.a.nseg;
         pl.a.nseg_div = FastDiv((uint32_t)pl.a.nseg);
@@ -1223,9 +1370,13 @@ int launch_plan(const BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream)
             return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                 constexpr bool SEQ = decltype(qc)::value;
                 const dim3 block(64 * kRowsWPB);
-                if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ>, grid, block, stream, a);
-                if (pl.vpt == 2) return launch(bwd_rows_vec<T, W, 2, SILU, SEQ>, grid, block, stream, a);
-                return launch(bwd_rows_vec<T, W, 1, SILU, SEQ>, grid, block, stream, a);
+                if (a.ragged) {
+                    if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ, true>, grid, block, stream, a);
+                    return launch(bwd_rows_vec<T, W, 1, SILU, SEQ, true>, grid, block, stream, a);
+                }
+                if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ, false>, grid, block, stream, a);
+                if (pl.vpt == 2) return launch(bwd_rows_vec<T, W, 2, SILU, SEQ, false>, grid, block, stream, a);
+                return launch(bwd_rows_vec<T, W, 1, SILU, SEQ, false>, grid, block, stream, a);
             });
         }
         return CC1D_ERR_SHAPE;  // not reached: the plan only picks rows when the halo fits

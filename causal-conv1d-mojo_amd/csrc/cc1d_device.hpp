@@ -200,6 +200,38 @@ template <typename T> __device__ __forceinline__ u32x4 vload_uniform(const T* p)
 }
 template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 
+// a[k] for a runtime k (0 outside [0, N)), as a chain of selects: a register
+// array indexed at run time would be placed in scratch memory
+template <int N> __device__ __forceinline__ float pick(const float* a, int k) {
+    float r = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) r = (i == k) ? a[i] : r;
+    return r;
+}
+
+// N (4 or 8) consecutive int32 values p[0 .. N) where p is r elements past a
+// 16-byte boundary (r the same for every lane): the aligned 16-byte vectors
+// covering them, each of which holds at least one of the N, so the accesses
+// stay inside whatever allocation holds p[0 .. N); then a shift by r.
+template <int N>
+__device__ __forceinline__ void load_i32_shifted(const int32_t* p, int r, int32_t* out) {
+    static_assert(N == 4 || N == 8, "one or two 16-byte vectors");
+    const u32x4* a = reinterpret_cast<const u32x4*>(p - r);
+    uint32_t c[N + 4];
+    const u32x4 v0 = a[0];
+    const u32x4 v1 = (N == 8 || r != 0) ? a[1] : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 v2 = (N == 8 && r != 0) ? a[N == 8 ? 2 : 1] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c[i] = v0[i];
+        c[4 + i] = v1[i];
+        if constexpr (N == 8) c[8 + i] = v2[i];
+    }
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+        out[e] = (int32_t)(r == 0 ? c[e] : r == 1 ? c[e + 1] : r == 2 ? c[e + 2] : c[e + 3]);
+}
+
 // SiLU = x * sigmoid(x), as x * rcp(1 + exp(-x)) in fp32.
 __device__ __forceinline__ float silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));

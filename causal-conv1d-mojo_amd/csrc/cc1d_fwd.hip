@@ -15,6 +15,13 @@
 //                    halo before a vector comes from the neighbouring lane
 //                    (ds_bpermute); only lane 0 of a segment reads one extra
 //                    vector from global memory. No LDS, no barriers.
+//                    Ragged rows (a start that is not 16-byte aligned, or a
+//                    length that is not a multiple of the vector) are read in
+//                    the 16-byte vectors of their own memory: a row that starts
+//                    m elements past a vector boundary is walked from that
+//                    boundary, its first m elements (the previous row's) are
+//                    replaced by initial_states or zero, and the vectors it
+//                    shares with its neighbours are stored element by element.
 //   fwd_cl        -- rows contiguous along channels (channel-last). A lane owns
 //                    4 bytes of adjacent channels, a wavefront a tile of 16
 //                    time steps (plus W-1 halo rows) of 64 lanes' channels,
@@ -28,6 +35,7 @@ namespace cc1d {
 
 struct FwdArgs {
     cc1d_fwd_params p;
+    int32_t ragged;    // rows_vec: rows may start off a 16-byte boundary / end inside a vector (kernel variant)
     FastDiv nseg_div;  // rows_vec: item -> row
     FastDiv dim_div;   // rows_vec: row -> batch entry
     int64_t nseg;     // segments (rows_vec), tiles (cl) or chunks (generic) per row
@@ -38,20 +46,26 @@ struct FwdArgs {
 
 // One wavefront-segment of one row. FULL: the whole segment lies inside the
 // row (no per-vector bounds checks).
-template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL>
+//
+// Positions t here count from the 16-byte boundary at or before the row's
+// first element: the row holds t in [m, m + L) (m = 0 for an aligned row), so
+// every vector access is aligned. A 16-byte vector that holds one of the
+// row's elements lies in the same memory page, so reading it whole is safe.
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool FULL, bool RAG>
 __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int lane, int64_t b, int64_t c,
-                                                 int32_t t0) {
+                                                 int32_t t0, int32_t m) {
     constexpr int EPV = elems16<T>::value;
     constexpr int H = W - 1;
     const int32_t L = (int32_t)p.seqlen;
-    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1];
-    T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1];
+    const int32_t Lv = L + m;  // end of the row
+    const T* __restrict__ xr = static_cast<const T*>(p.x) + b * p.x_stride[0] + c * p.x_stride[1] - m;
+    T* __restrict__ orow = static_cast<T*>(p.out) + b * p.out_stride[0] + c * p.out_stride[1] - m;
 
     u32x4 v[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int32_t t = t0 + (j * 64 + lane) * EPV;
-        v[j] = (FULL || t < L) ? vload_nt(xr + t) : vzero();
+        v[j] = (FULL || t < Lv) ? vload_nt(xr + t) : vzero();
     }
     u32x4 h = vzero();
     if (lane == 0 && t0 > 0) h = vload(xr - EPV + t0);
@@ -59,21 +73,36 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
     int32_t id[VPT][EPV];
     int32_t hid[H];
     if constexpr (SEQ) {
-        const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
+        const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];  // unit time stride
+        // ragged rows: a vector's ids start rid ids past a 16-byte boundary
+        // (its first position, t - m, is a multiple of 4 plus -m)
+        const int rid = RAG ? (int)uniform32(((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) - (uint32_t)m) & 3u) : 0;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int32_t t = t0 + (j * 64 + lane) * EPV;
+            if constexpr (!RAG) {  // aligned rows: 16-byte vectors of 4 ids
 #pragma unroll
-            for (int q = 0; q < EPV / 4; ++q) {
-                const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
-                                                : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+                for (int q = 0; q < EPV / 4; ++q) {
+                    const u32x4 s = (FULL || t < L) ? *reinterpret_cast<const u32x4*>(sr + t + 4 * q)
+                                                    : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
+                    for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
+                }
+            } else if (FULL || (t >= m && t + EPV <= Lv)) {  // every position inside the row
+                load_i32_shifted<EPV>(sr + (t - m), rid, id[j]);
+            } else {  // one id per position; -1 outside the row
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    const int32_t pos = t + e - m;
+                    id[j][e] = (pos >= 0 && pos < L) ? sr[pos] : -1;
+                }
             }
         }
 #pragma unroll
-        for (int i = 0; i < H; ++i)
-            hid[i] = (lane == 0 && t0 - H + i >= 0) ? sr[t0 - H + i] : -1;
+        for (int i = 0; i < H; ++i) {
+            const int32_t pos = t0 - H + i - m;
+            hid[i] = (lane == 0 && pos >= 0) ? sr[pos] : -1;
+        }
     }
 
     float w[W];
@@ -92,6 +121,15 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
                           b * p.initial_states_stride[0] + c * p.initial_states_stride[1] +
                               i * p.initial_states_stride[2]);
     }
+    // the row's first vector holds m elements of the previous row: they are
+    // positions -m .. -1 of this one (initial_states or zero)
+    if (RAG && !FULL && t0 == 0 && m > 0 && lane == 0) {
+        float f[EPV];
+#pragma unroll
+        for (int e = 0; e < EPV; ++e)  // initial_states slot e - m + H (none when negative)
+            f[e] = e >= m ? vget<T>(v[0], e) : pick<H>(hinit, e - m + H);
+        v[0] = vpack<T>(f);
+    }
 
     constexpr int D0 = ((EPV - H) * (int)sizeof(T)) / 4;  // first dword of the needed tail
     const int prev_lane = (lane + 63) & 63;
@@ -106,8 +144,14 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
         }
         if (j == 0 && lane == 0) pv = h;
         float win[H + EPV];
+        // before the row (t0 == 0, lane 0): position i - H - m, initial_states slot i - m
 #pragma unroll
-        for (int i = 0; i < H; ++i) win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
+        for (int i = 0; i < H; ++i) {
+            if constexpr (FULL || !RAG)  // m == 0 whenever a first segment is full
+                win[i] = (j == 0 && use_init) ? hinit[i] : vget<T>(pv, EPV - H + i);
+            else
+                win[i] = (j == 0 && use_init) ? pick<H>(hinit, i - m) : vget<T>(pv, EPV - H + i);
+        }
 #pragma unroll
         for (int i = 0; i < EPV; ++i) win[H + i] = vget<T>(v[j], i);
 
@@ -136,16 +180,27 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
             }
             o[i] = acc;
         }
-        if (FULL || t < L) vstore_nt(orow + t, vpack<T>(o));
+        if constexpr (!RAG) {
+            if (FULL || t < L) vstore_nt(orow + t, vpack<T>(o));
+        } else if (FULL || (t >= m && t + EPV <= Lv)) {
+            vstore_nt(orow + t, vpack<T>(o));
+        } else if (t < Lv) {  // a vector shared with a neighbouring row
+#pragma unroll
+            for (int e = 0; e < EPV; ++e)
+                if (t + e >= m && t + e < Lv) st(orow, t + e, o[e]);
+        }
 
-        // final_states (_fn.py:31-50): the lane holding position L-1 owns the
-        // last W-1 columns (L % EPV == 0 on this path, so they are win[EPV..]).
-        if (p.final_states_out != nullptr && t + EPV == L) {
+        // final_states (_fn.py:31-50): the lane holding the row's last
+        // position writes the last W-1 columns from its window (they are
+        // positions t - H .. t + EPV - 1)
+        if (p.final_states_out != nullptr && (RAG ? (t < Lv && Lv <= t + EPV) : t + EPV == L)) {
             T* fs = static_cast<T*>(p.final_states_out) + b * p.final_states_stride[0] +
                     c * p.final_states_stride[1];
 #pragma unroll
-            for (int i = 0; i < H; ++i)
-                st(fs, i * p.final_states_stride[2], (L - H + i >= 0) ? win[EPV + i] : 0.0f);
+            for (int i = 0; i < H; ++i) {  // position L - H + i is window slot Lv + i - t
+                const float v = RAG ? pick<H + EPV>(win, Lv + i - t) : win[EPV + i];  // aligned: t + EPV == L
+                st(fs, i * p.final_states_stride[2], (L - H + i >= 0) ? v : 0.0f);
+            }
         }
     }
 }
@@ -153,7 +208,7 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
 // Item = (row, segment) with row = b * dim + c; four wavefronts per block take
 // four consecutive items, i.e. adjacent segments of a row or adjacent rows.
 // All index arithmetic is 32-bit (the launcher checks the ranges).
-template <typename T, int W, int VPT, bool SILU, bool SEQ>
+template <typename T, int W, int VPT, bool SILU, bool SEQ, bool RAG>
 __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
     constexpr int SEG = 64 * VPT * elems16<T>::value;
     const cc1d_fwd_params& p = a.p;
@@ -165,8 +220,19 @@ __global__ void __launch_bounds__(256) fwd_rows_vec(const FwdArgs a) {
     const int32_t t0 = (int32_t)((item - row * (uint32_t)a.nseg) * SEG);
     const uint32_t b = a.dim_div.div(row);
     const uint32_t c = row - b * (uint32_t)p.dim;
-    if (t0 + SEG <= (int32_t)p.seqlen) fwd_rows_segment<T, W, VPT, SILU, SEQ, true>(p, lane, b, c, t0);
-    else fwd_rows_segment<T, W, VPT, SILU, SEQ, false>(p, lane, b, c, t0);
+    constexpr int EPV = elems16<T>::value;
+    // ragged rows: the row starts m elements past a 16-byte boundary
+    int32_t m = 0;
+    if constexpr (RAG) {
+        const T* xrow = static_cast<const T*>(p.x) + (int64_t)b * p.x_stride[0] + (int64_t)c * p.x_stride[1];
+        m = (int32_t)uniform32((uint32_t)(reinterpret_cast<uintptr_t>(xrow) / sizeof(T)) & (EPV - 1));
+    }
+    const int32_t Lv = (int32_t)p.seqlen + m;
+    if (RAG && t0 >= Lv) return;  // the row ends before this segment
+    if ((t0 > 0 || m == 0) && t0 + SEG <= Lv)
+        fwd_rows_segment<T, W, VPT, SILU, SEQ, true, RAG>(p, lane, b, c, t0, m);
+    else
+        fwd_rows_segment<T, W, VPT, SILU, SEQ, false, RAG>(p, lane, b, c, t0, m);
 }
 
 // Channel-last (unit channel stride), tiled: a lane owns CPL adjacent
@@ -399,6 +465,26 @@ bool rows_vec_ok(const cc1d_fwd_params& p) {
     return true;
 }
 
+// ragged rows (a seqlen that is not a multiple of the vector, or rows that do
+// not start on a 16-byte boundary): unit time stride, and out laid out like x
+// modulo the vector -- the same element strides modulo EPV and bases a
+// multiple of 16 bytes apart -- so every row of out starts as far past a
+// 16-byte boundary as its row of x; seq_idx with a unit time stride
+template <typename T>
+bool rows_ragged_ok(const cc1d_fwd_params& p) {
+    constexpr int64_t EPV = elems16<T>::value;
+    if (p.width - 1 > EPV) return false;
+    if (p.x_stride[2] != 1 || p.out_stride[2] != 1) return false;
+    if ((p.out_stride[0] - p.x_stride[0]) % EPV != 0 || (p.out_stride[1] - p.x_stride[1]) % EPV != 0) return false;
+    if ((reinterpret_cast<intptr_t>(p.out) - reinterpret_cast<intptr_t>(p.x)) % 16 != 0) return false;
+    if (p.seq_idx != nullptr && (p.seq_idx_stride[1] != 1 || reinterpret_cast<uintptr_t>(p.seq_idx) % 4 != 0))
+        return false;
+    const int64_t lim = (int64_t)1 << 31;
+    if (p.seqlen + 64 * 4 * EPV + EPV >= lim) return false;
+    if (p.batch * p.dim * ceil_div(p.seqlen + EPV, 64 * EPV) * 4 >= ((int64_t)1 << 32)) return false;
+    return true;
+}
+
 // channel-last tiles: unit channel stride, CPL | dim, rows aligned to the
 // CPL-channel lane vector, 32-bit positions inside a batch
 template <typename T, int CPL>
@@ -430,12 +516,18 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                 a.p = p;
                 a.chunk = 0;
                 a.ngroups = 0;
+                a.ragged = 0;
                 const int64_t rows = p.batch * p.dim;
                 if constexpr (W - 1 <= EPV) {
-                    if (rows_vec_ok<T>(p)) {
-                        const int64_t nvec = p.seqlen / EPV;
+                    const bool aligned = rows_vec_ok<T>(p);
+                    if (aligned || rows_ragged_ok<T>(p)) {
+                        a.ragged = aligned ? 0 : 1;
+                        // vectors a row spans: a ragged row may start up to EPV - 1
+                        // elements past a vector boundary
+                        const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
                         const int64_t per = ceil_div(nvec, 64);
-                        const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+                        // (the ragged kernels are built for 4 and 1 vectors per lane only)
+                        const int vpt = per >= 4 ? 4 : (per >= 2 && aligned ? 2 : 1);
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
                         a.nseg_div = FastDiv((uint32_t)a.nseg);
@@ -443,9 +535,13 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                             constexpr bool SEQ = decltype(qc)::value;
-                            if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ>, grid, dim3(256), stream, a);
-                            if (vpt == 2) return launch(fwd_rows_vec<T, W, 2, SILU, SEQ>, grid, dim3(256), stream, a);
-                            return launch(fwd_rows_vec<T, W, 1, SILU, SEQ>, grid, dim3(256), stream, a);
+                            if (a.ragged) {
+                                if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ, true>, grid, dim3(256), stream, a);
+                                return launch(fwd_rows_vec<T, W, 1, SILU, SEQ, true>, grid, dim3(256), stream, a);
+                            }
+                            if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ, false>, grid, dim3(256), stream, a);
+                            if (vpt == 2) return launch(fwd_rows_vec<T, W, 2, SILU, SEQ, false>, grid, dim3(256), stream, a);
+                            return launch(fwd_rows_vec<T, W, 1, SILU, SEQ, false>, grid, dim3(256), stream, a);
                         });
                     }
                 }

@@ -197,10 +197,11 @@ def test_varlen_validation_codes(lib):
     assert call(batch=0) == OK
 
 
-def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4):
+def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4, offsets=(0, 0, 0)):
     p = _lib.BwdParams()
-    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the size is computed on the host
-    p.x = p.weight = p.dout = p.dx = fake
+    fake = 1 << 20  # never dereferenced: the size is computed on the host
+    p.x, p.dout, p.dx = (ctypes.c_void_p(fake + o) for o in offsets)  # byte offsets
+    p.weight = ctypes.c_void_p(fake)
     p.batch, p.dim, p.seqlen, p.width = B, D, L, W
     strides = (D * L, 1, D) if channel_last else (D * L, L, 1)
     p.x_stride[:] = p.dout_stride[:] = p.dx_stride[:] = strides
@@ -220,3 +221,33 @@ def test_workspace_sizes_of_the_benchmark_configurations(lib):
     }
     assert sizes == {"C2": 102_400, "C3": 163_840, "C5 bf16": 655_360, "C5 fp32": 1_310_720}
     assert max(sizes.values()) <= _lib.NOALLOC_WORKSPACE_FLOATS == 2_097_152
+
+
+def test_ragged_rows_keep_the_row_kernel(lib):
+    """Rows whose length is not a multiple of the 16-byte vector, or that start off a 16-byte
+    boundary, are planned as row segments (one record of W + 1 floats per segment of 64 lanes
+    x VPT vectors, spanning ceil((L + EPV - 1) / EPV) vectors); the generic kernel would take
+    64-step chunks. dout or dx at another offset modulo 16 bytes falls back to it."""
+    B, D, W = 1, 64, 4
+
+    def rows(L, epv, aligned=False):
+        nvec = L // epv if aligned else -(-(L + epv - 1) // epv)
+        per = -(-nvec // 64)
+        vpt = 4 if per >= 4 else (2 if per >= 2 and aligned else 1)
+        return B * D * -(-nvec // (64 * vpt)) * (W + 1)
+
+    def generic(L):
+        return B * D * -(-L // 64) * (W + 1)
+
+    bf16, fp32 = 1, 2
+    assert _workspace_floats(lib, B, D, 2048, bf16) == rows(2048, 8, aligned=True) == 320
+    assert _workspace_floats(lib, B, D, 2047, bf16) == rows(2047, 8) == 640
+    assert _workspace_floats(lib, B, D, 1001, bf16) == rows(1001, 8) == 640
+    assert _workspace_floats(lib, B, D, 7, bf16) == rows(7, 8) == 320
+    assert _workspace_floats(lib, B, D, 2047, fp32) == rows(2047, 4) == 960
+    # a base one element past a 16-byte boundary, x / dout / dx alike
+    assert _workspace_floats(lib, B, D, 2048, bf16, offsets=(2, 2, 2)) == rows(2048, 8) == 640
+    assert _workspace_floats(lib, B, D, 2048, fp32, offsets=(4, 4, 4)) == rows(2048, 4) == 960
+    # dout at another offset inside its vector than x: the generic kernel
+    assert _workspace_floats(lib, B, D, 2047, bf16, offsets=(0, 2, 0)) == generic(2047) == 10240
+    assert _workspace_floats(lib, B, D, 2048, bf16, offsets=(2, 2, 4)) == generic(2048) == 10240
