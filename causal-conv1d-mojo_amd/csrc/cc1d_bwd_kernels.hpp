@@ -155,7 +155,9 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         const int next_lane = (lane + 1) & 63;
 
         // ---- dpre of vector j + dweight/dbias partials ----
-        auto dpre_vec = [&](const int j, float* dpj) {
+        // PART: some lane's vector j may hold a position outside the row
+        auto dpre_vec = [&](const int j, float* dpj, auto part_c) {
+            constexpr bool PART = decltype(part_c)::value;
             const int32_t t = t0 + (j * 64 + lane) * EPV;
             u32x4 pv = vzero();
 #pragma unroll
@@ -193,7 +195,7 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
                 // to the weight gradient (a select, not a product with zero,
                 // which a non-finite x there would turn into NaN). Aligned
                 // rows end on a vector boundary: the test is the vector's.
-                const bool outside = !FULL && (RAG ? (t + i < m || t + i >= L) : t >= L);
+                const bool outside = PART && (RAG ? (t + i < m || t + i >= L) : t >= L);
                 if (outside) d = 0.0f;
                 dpj[i] = d;
                 pb += d;
@@ -262,7 +264,15 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         float dp[2][EPV];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            dpre_vec(j, dp[j & 1]);
+            if constexpr (RAG && !FULL) {
+                // a ragged row's segments are not full, but only their first and
+                // last vectors hold positions outside the row (wave-uniform test)
+                const int32_t vs = t0 + j * 64 * EPV;  // vector j of lane 0
+                if (vs >= m && vs + 64 * EPV <= L) dpre_vec(j, dp[j & 1], std::false_type{});
+                else dpre_vec(j, dp[j & 1], std::true_type{});
+            } else {
+                dpre_vec(j, dp[j & 1], std::bool_constant<!FULL>{});
+            }
             if (j == 0 && p.dinitial_states != nullptr && t0 == 0) {  // wave-uniform
                 // dinitial_states (bwd_full_cpu/kernel.mojo:210-219) from dpre of
                 // positions 0 .. H-1: elements m .. m+H-1 of lane 0's first
@@ -1329,8 +1339,7 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
         const int64_t per = ceil_div(nvec, 64);
         pl.kind = kBwdRows;
-        // (the ragged kernels are built for 4 and 1 vectors per lane only)
-        pl.vpt = per >= 4 ? 4 : (per >= 2 && aligned ? 2 : 1);
+        pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
         pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
         pl.a.n_items = p.batch * p.dim * pl.a.nseg;
         pl.a.nseg_div = FastDiv((uint32_t)pl.a.nseg);
@@ -1370,13 +1379,12 @@ int launch_plan(const BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream)
             return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                 constexpr bool SEQ = decltype(qc)::value;
                 const dim3 block(64 * kRowsWPB);
-                if (a.ragged) {
-                    if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ, true>, grid, block, stream, a);
-                    return launch(bwd_rows_vec<T, W, 1, SILU, SEQ, true>, grid, block, stream, a);
-                }
-                if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ, false>, grid, block, stream, a);
-                if (pl.vpt == 2) return launch(bwd_rows_vec<T, W, 2, SILU, SEQ, false>, grid, block, stream, a);
-                return launch(bwd_rows_vec<T, W, 1, SILU, SEQ, false>, grid, block, stream, a);
+                return with_flag(a.ragged != 0, [&](auto rc) {
+                    constexpr bool RAG = decltype(rc)::value;
+                    if (pl.vpt == 4) return launch(bwd_rows_vec<T, W, 4, SILU, SEQ, RAG>, grid, block, stream, a);
+                    if (pl.vpt == 2) return launch(bwd_rows_vec<T, W, 2, SILU, SEQ, RAG>, grid, block, stream, a);
+                    return launch(bwd_rows_vec<T, W, 1, SILU, SEQ, RAG>, grid, block, stream, a);
+                });
             });
         }
         return CC1D_ERR_SHAPE;  // not reached: the plan only picks rows when the halo fits

@@ -526,8 +526,7 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         // elements past a vector boundary
                         const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
                         const int64_t per = ceil_div(nvec, 64);
-                        // (the ragged kernels are built for 4 and 1 vectors per lane only)
-                        const int vpt = per >= 4 ? 4 : (per >= 2 && aligned ? 2 : 1);
+                        const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
                         a.nseg_div = FastDiv((uint32_t)a.nseg);
@@ -535,13 +534,12 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         const dim3 grid((unsigned)ceil_div(a.n_items, 4));
                         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
                             constexpr bool SEQ = decltype(qc)::value;
-                            if (a.ragged) {
-                                if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ, true>, grid, dim3(256), stream, a);
-                                return launch(fwd_rows_vec<T, W, 1, SILU, SEQ, true>, grid, dim3(256), stream, a);
-                            }
-                            if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ, false>, grid, dim3(256), stream, a);
-                            if (vpt == 2) return launch(fwd_rows_vec<T, W, 2, SILU, SEQ, false>, grid, dim3(256), stream, a);
-                            return launch(fwd_rows_vec<T, W, 1, SILU, SEQ, false>, grid, dim3(256), stream, a);
+                            return with_flag(a.ragged != 0, [&](auto rc) {
+                                constexpr bool RAG = decltype(rc)::value;
+                                if (vpt == 4) return launch(fwd_rows_vec<T, W, 4, SILU, SEQ, RAG>, grid, dim3(256), stream, a);
+                                if (vpt == 2) return launch(fwd_rows_vec<T, W, 2, SILU, SEQ, RAG>, grid, dim3(256), stream, a);
+                                return launch(fwd_rows_vec<T, W, 1, SILU, SEQ, RAG>, grid, dim3(256), stream, a);
+                            });
                         });
                     }
                 }

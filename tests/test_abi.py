@@ -233,7 +233,7 @@ def test_ragged_rows_keep_the_row_kernel(lib):
     def rows(L, epv, aligned=False):
         nvec = L // epv if aligned else -(-(L + epv - 1) // epv)
         per = -(-nvec // 64)
-        vpt = 4 if per >= 4 else (2 if per >= 2 and aligned else 1)
+        vpt = 4 if per >= 4 else (2 if per >= 2 else 1)
         return B * D * -(-nvec // (64 * vpt)) * (W + 1)
 
     def generic(L):
@@ -242,7 +242,7 @@ def test_ragged_rows_keep_the_row_kernel(lib):
     bf16, fp32 = 1, 2
     assert _workspace_floats(lib, B, D, 2048, bf16) == rows(2048, 8, aligned=True) == 320
     assert _workspace_floats(lib, B, D, 2047, bf16) == rows(2047, 8) == 640
-    assert _workspace_floats(lib, B, D, 1001, bf16) == rows(1001, 8) == 640
+    assert _workspace_floats(lib, B, D, 1001, bf16) == rows(1001, 8) == 320
     assert _workspace_floats(lib, B, D, 7, bf16) == rows(7, 8) == 320
     assert _workspace_floats(lib, B, D, 2047, fp32) == rows(2047, 4) == 960
     # a base one element past a 16-byte boundary, x / dout / dx alike
