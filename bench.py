@@ -359,6 +359,41 @@ def _c2_seq_cases(torch, sets, w, b):
     }
 
 
+LR = L - 7  # 2041: not a multiple of the 8-element (16-byte) vector
+
+
+def _c2_ragged_cases(torch, w, b, nsets=4):
+    """C2's shape at seqlen 2041: contiguous rows of an odd length start at every offset inside
+    their 16-byte vector, so the row kernels' ragged instantiation runs (own buffer sets, as
+    many as C2's)."""
+    ops = torch.ops.causal_conv1d_amd
+    bufs = []
+    for i in range(nsets):
+        g = torch.Generator(device="cuda").manual_seed(300 + i)
+        x = torch.randn(B, D, LR, generator=g, device="cuda").bfloat16()
+        dout = torch.randn(B, D, LR, generator=g, device="cuda").bfloat16()
+        bufs.append((x, dout, torch.empty_like(x), torch.empty_like(x)))
+    dw = torch.zeros(D, W, dtype=torch.float32, device="cuda")
+    db = torch.zeros(D, dtype=torch.float32, device="cuda")
+    dwt = torch.empty(D, W, dtype=torch.bfloat16, device="cuda")
+    dbt = torch.empty(D, dtype=torch.bfloat16, device="cuda")
+    act = B * D * LR * 2  # one activation tensor
+    fwd_bytes = 2 * act + D * W * 2 + D * 2
+    bwd_bytes = 3 * act + D * W * 2 + D * 2 + D * W * 4 + D * 4
+    typed_bytes = 3 * act + D * W * 2 + D * 2 + D * W * 2 + D * 2
+    note = {"workload": f"C2 shape at seqlen {LR} (4 x 5120 x {LR} bf16, W4, bias, SiLU): ragged rows"}
+    return {
+        "fwd_ragged": ([lambda x=x, o=o: ops._fwd_inplace(x, w, b, None, None, o, True, None)
+                        for x, _, o, _ in bufs], fwd_bytes, 1, note),
+        "bwd_ragged": ([lambda x=x, d=d, dx=dx: ops._bwd_full_inplace(x, w, b, d, None, None, dx, dw, db, None,
+                                                                       True)
+                        for x, d, _, dx in bufs], bwd_bytes, 1, note),
+        "bwd_typed_ragged": ([lambda x=x, d=d, dx=dx: ops._bwd_typed_inplace(x, w, b, d, None, None, None, dx,
+                                                                              dwt, dbt, None, True)
+                              for x, d, _, dx in bufs], typed_bytes, 1, note),
+    }
+
+
 def _c2_floor_cases(torch, sets, floors):
     """The C2 backward's streams with no arithmetic: x and dout read, dx written, on the
     same sets viewed as (B * D) rows of 4 KB: a wavefront per 4 rows x 1 KB, or per row
@@ -679,6 +714,7 @@ def mode_kernels(torch, cc, floors, args):
     cases.update(_c4a_cases(torch, cc, floors))
     if not args.no_configs:
         cases.update(_c2_seq_cases(torch, sets, w, b))
+        cases.update(_c2_ragged_cases(torch, w, b))
         c3, c3info = _c3_cases(torch, floors)
         cases.update(c3)
         cases.update(_c5_cases(torch))
@@ -730,6 +766,7 @@ def main():
     _run_cases(torch, _c2_floor_cases(torch, sets, floors), args, kern)
     if not args.no_configs:
         _run_cases(torch, _c2_seq_cases(torch, sets, w, b), args, kern)
+        _run_cases(torch, _c2_ragged_cases(torch, w, b, nsets), args, kern)
     for k in ("fwd", "bwd", "bwd_typed"):
         kern[k]["buffer_sets"] = nsets
     kern["fwd"]["floor_copy_us"] = kern["floor_copy_c2"]["us_per_launch"]

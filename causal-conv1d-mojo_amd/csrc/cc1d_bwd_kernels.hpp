@@ -1063,7 +1063,11 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
                     }
                     if (dead) d = 0.0f;
                     dn[e] = d;
-                    if constexpr (ACC) {
+                    // a step past the end adds no term (zero dpre times a
+                    // non-finite x of the window would be NaN); padding
+                    // inside the sequence adds its zero terms, as the
+                    // reference does (wave-uniform test)
+                    if (ACC && in) {
                         s.pb[e] += d;
 #pragma unroll
                         for (int k = 0; k < H; ++k)

@@ -37,19 +37,21 @@ def _skip_fp32_wide(dtype, width):
         pytest.skip("fp32 widths above 5 are rejected by the API (reference _fn.py:405-414)")
 
 
-def _autograd(x, w, b, dout, *, init=None, seq_idx=None, dfs=None, activation="silu"):
-    """Forward + backward through the public API on the GPU: (out, final_states, dx, dw, db, dinit)."""
+def _autograd(x, w, b, dout, *, init=None, seq_idx=None, dfs=None, activation="silu", view=None):
+    """Forward + backward through the public API on the GPU (x through a layout `view`):
+    (out, final_states, dx, dw, db, dinit)."""
     xg = x.to(DEV).requires_grad_()
     wg = w.to(DEV).requires_grad_()
     bg = b.to(DEV).requires_grad_() if b is not None else None
     ig = init.to(DEV).requires_grad_() if init is not None else None
     kw = dict(initial_states=ig, activation=activation, seq_idx=None if seq_idx is None else seq_idx.to(DEV))
     fs = None
+    xin = xg if view is None else view(xg)
     if dfs is not None:
-        out, fs = cc.causal_conv1d_fn(xg, wg, bg, return_final_states=True, **kw)
+        out, fs = cc.causal_conv1d_fn(xin, wg, bg, return_final_states=True, **kw)
         torch.autograd.backward([out, fs], [dout.to(DEV), dfs.to(DEV)])
     else:
-        out = cc.causal_conv1d_fn(xg, wg, bg, **kw)
+        out = cc.causal_conv1d_fn(xin, wg, bg, **kw)
         out.backward(dout.to(DEV))
     torch.cuda.synchronize()
     cpu = (lambda t: None if t is None else t.detach().cpu())
@@ -199,14 +201,23 @@ def _same_nonfinite_then_close(got, ref, dtype, name, scale=None):
         assert_reduction_close(got[fin], ref[fin], dtype, scale=scale[fin], name=name)
 
 
+_LAYOUTS = {
+    "rows": None,
+    "channel_last": lambda t: t.transpose(1, 2).contiguous().transpose(1, 2),
+    "strided": lambda t: torch.stack([t, t], -1)[..., 0],
+}
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("seqlen", [1021, 1032])
 @pytest.mark.parametrize("mode", ["linear", "silu", "seq_idx"])
-def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode):
-    """Channel 2 ends in inf, channel 5 starts with NaN, channel 8 is NaN throughout: each
+@pytest.mark.parametrize("layout", list(_LAYOUTS))
+def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode, layout):
+    """Channel 2 ends in inf, channel 5 starts with NaN, channel 8 is NaN throughout. Rows: each
     shares vectors with its neighbours (1021: ragged rows), or is the last row of a segment
-    that lies past the row's end (1032: aligned rows). Only the entries that the reference
-    makes non-finite may be non-finite; everything else matches it."""
+    that lies past the row's end (1032: aligned rows). Channel-last: the last run of 128 steps
+    reaches past the end. Only the entries that the reference makes non-finite may be
+    non-finite; everything else matches it."""
     B, D, W = 2, 12, 4
     x, w, b, _ = make_inputs(B, D, seqlen, W, dtype=dtype)
     dout = make_inputs(B, D, seqlen, W, dtype=dtype, seed=1)[0]
@@ -218,7 +229,7 @@ def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode):
         clean[:, c] = 0
     act = "silu" if mode != "linear" else None
     seq = _leading_padding(B, seqlen) if mode == "seq_idx" else None
-    out, _, dx, dw, db, _ = _autograd(x, w, b, dout, seq_idx=seq, activation=act)
+    out, _, dx, dw, db, _ = _autograd(x, w, b, dout, seq_idx=seq, activation=act, view=_LAYOUTS[layout])
     rout = O.causal_conv1d_fn(x, w, b, seq_idx=seq, activation=act)
     rdx, rdw, rdb, _ = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=seq, activation=act)
     sw, sb = scales(clean, w, b, dout, seq_idx=seq, activation=act)
