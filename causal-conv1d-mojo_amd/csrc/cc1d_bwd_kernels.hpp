@@ -362,8 +362,10 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
     T* __restrict__ dxr = static_cast<T*>(p.dx) + b * p.dx_stride[0] + c * p.dx_stride[1] - m;
     const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];
     // (unit time stride) ragged rows: a vector's ids start rid ids past a
-    // 16-byte boundary (its first position, t - m, is a multiple of 4 plus -m)
-    const int rid = RAG ? (int)uniform32(((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) - (uint32_t)m) & 3u) : 0;
+    // 16-byte boundary (its first position, t - m, is a multiple of 4 plus
+    // -m); the row's first id a0 past one
+    const int a0 = RAG ? (int)uniform32((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) & 3u) : 0;
+    const int rid = (a0 - m) & 3;
     const int prev_lane = (lane + 63) & 63;
     const int next_lane = (lane + 1) & 63;
     // a ragged row's first vector holds m elements of the previous row: x
@@ -379,6 +381,7 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
     // ids: the lane's positions (-1 outside the row), and the H before and
     // after the segment (wave-uniform, -1 outside the row)
     int32_t id[VPT][EPV];
+    IdsRaw<EPV> raw[RAG ? VPT : 1];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int32_t t = t0 + (j * 64 + lane) * EPV;
@@ -390,15 +393,13 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
 #pragma unroll
                 for (int e = 0; e < 4; ++e) id[j][4 * q + e] = (int32_t)sv[e];
             }
-        } else if (FULL || (t >= m && t + EPV <= L)) {  // every position inside the row
-            load_i32_shifted<EPV>(sr + (t - m), rid, id[j]);
-        } else {  // one id per position; -1 outside the row
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const int32_t pos = t + e - m;
-                id[j][e] = (pos >= 0 && pos < Lr) ? sr[pos] : -1;
-            }
+        } else {
+            ids_load<EPV, !FULL>(sr, Lr, t - m, rid, a0, raw[j]);
         }
+    }
+    if constexpr (RAG) {  // -1 outside the row
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) ids_shift<EPV, !FULL>(raw[j], Lr, t0 + (j * 64 + lane) * EPV - m, rid, id[j]);
     }
     int32_t hid[H], nid[H];
 #pragma unroll

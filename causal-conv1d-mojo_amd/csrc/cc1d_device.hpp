@@ -209,27 +209,80 @@ template <int N> __device__ __forceinline__ float pick(const float* a, int k) {
     return r;
 }
 
-// N (4 or 8) consecutive int32 values p[0 .. N) where p is r elements past a
-// 16-byte boundary (r the same for every lane): the aligned 16-byte vectors
-// covering them, each of which holds at least one of the N, so the accesses
-// stay inside whatever allocation holds p[0 .. N); then a shift by r.
-template <int N>
-__device__ __forceinline__ void load_i32_shifted(const int32_t* p, int r, int32_t* out) {
+// Wavefront-uniform value (lets the compiler keep it in an SGPR).
+__device__ __forceinline__ uint32_t uniform32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uniform_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// A per-lane value the compiler can neither see through nor move: address
+// arithmetic of a rarely taken branch that uses it stays inside the branch
+// instead of being hoisted out of the loop around it (where it would hold
+// registers for the whole loop).
+__device__ __forceinline__ int32_t opaque(int32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// The N (4 or 8) ids of row positions pos .. pos + N - 1 of one seq_idx row
+// (sr, L ids, unit stride; -1 outside [0, L)), read as the N/4 + 1 aligned
+// 16-byte vectors that cover them (ids_load) and shifted into place
+// (ids_shift): r = the first id's offset in its vector (the same for every
+// lane), a0 = sr's own offset in its vector. MASK: some position may lie
+// outside the row; a lane with none inside loads nothing, and a vector that
+// holds none of the row's ids reads the row's first vector instead, as does
+// the last one when r == 0 (not needed then), so every access stays inside
+// the row's allocation. A kernel issues every vector's loads before the
+// first shift: a shift right behind its loads waits for them, before the
+// next vector's loads are issued.
+template <int N> struct IdsRaw {
+    u32x4 v[N / 4 + 1];
+};
+
+template <int N, bool MASK>
+__device__ __forceinline__ void ids_load(const int32_t* sr, int32_t L, int32_t pos, int r, int a0, IdsRaw<N>& raw) {
     static_assert(N == 4 || N == 8, "one or two 16-byte vectors");
-    const u32x4* a = reinterpret_cast<const u32x4*>(p - r);
-    uint32_t c[N + 4];
-    const u32x4 v0 = a[0];
-    const u32x4 v1 = (N == 8 || r != 0) ? a[1] : u32x4{0u, 0u, 0u, 0u};
-    const u32x4 v2 = (N == 8 && r != 0) ? a[N == 8 ? 2 : 1] : u32x4{0u, 0u, 0u, 0u};
+    constexpr int NV = N / 4 + 1;
+    const int32_t q0 = pos - r;  // first row position of the first vector (16-byte aligned)
+    if (!MASK || (pos + N > 0 && pos < L)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        c[i] = v0[i];
-        c[4 + i] = v1[i];
-        if constexpr (N == 8) c[8 + i] = v2[i];
+        for (int v = 0; v < NV; ++v) {
+            int32_t q = q0 + 4 * v;
+            if (v == NV - 1) q = r != 0 ? q : q0;
+            if constexpr (MASK) q = (q + 3 >= 0 && q < L) ? q : -a0;
+            raw.v[v] = *reinterpret_cast<const u32x4*>(sr + q);
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) raw.v[v] = vzero();  // masked to -1 by ids_shift
     }
+}
+
+// The shift is two levels of v_perm_b32 (one dword of two, by the bits of
+// r): selects on a scalar r became branches, each waiting for its loads, and
+// selects on a vector-register r an indexed copy through scratch memory.
+template <int N, bool MASK>
+__device__ __forceinline__ void ids_shift(const IdsRaw<N>& raw, int32_t L, int32_t pos, int r, int32_t* out) {
+    uint32_t c[N + 4];
 #pragma unroll
-    for (int e = 0; e < N; ++e)
-        out[e] = (int32_t)(r == 0 ? c[e] : r == 1 ? c[e + 1] : r == 2 ? c[e + 2] : c[e + 3]);
+    for (int v = 0; v < N / 4 + 1; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c[4 * v + i] = raw.v[v][i];
+    // byte selectors of v_perm_b32(hi, lo, sel): 0x07060504 picks hi, 0x03020100 lo
+    const uint32_t s2 = (r & 2) ? 0x07060504u : 0x03020100u;
+    const uint32_t s1 = (r & 1) ? 0x07060504u : 0x03020100u;
+    uint32_t t[N + 2];
+#pragma unroll
+    for (int e = 0; e < N + 2; ++e) t[e] = __builtin_amdgcn_perm(c[e + 2], c[e], s2);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+        out[e] = (int32_t)__builtin_amdgcn_perm(t[e + 1], t[e], s1);
+        if constexpr (MASK) out[e] = (pos + e >= 0 && pos + e < L) ? out[e] : -1;
+    }
 }
 
 // SiLU = x * sigmoid(x), as x * rcp(1 + exp(-x)) in fp32.
@@ -316,25 +369,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<kDppRowBcast15, 0xa>(v);
     v += dpp_f32<kDppRowBcast31, 0xc>(v);
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Wavefront-uniform value (lets the compiler keep it in an SGPR).
-__device__ __forceinline__ uint32_t uniform32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ float uniform_f32(float v) {
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
-}
-__device__ __forceinline__ int64_t uniform(int64_t v) {
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-// A per-lane value the compiler can neither see through nor move: address
-// arithmetic of a rarely taken branch that uses it stays inside the branch
-// instead of being hoisted out of the loop around it (where it would hold
-// registers for the whole loop).
-__device__ __forceinline__ int32_t opaque(int32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
 }
 
 }  // namespace cc1d

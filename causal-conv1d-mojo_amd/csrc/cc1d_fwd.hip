@@ -75,8 +75,11 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
     if constexpr (SEQ) {
         const int32_t* __restrict__ sr = p.seq_idx + b * p.seq_idx_stride[0];  // unit time stride
         // ragged rows: a vector's ids start rid ids past a 16-byte boundary
-        // (its first position, t - m, is a multiple of 4 plus -m)
-        const int rid = RAG ? (int)uniform32(((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) - (uint32_t)m) & 3u) : 0;
+        // (its first position, t - m, is a multiple of 4 plus -m); the row's
+        // first id a0 past one
+        const int a0 = RAG ? (int)uniform32((uint32_t)(reinterpret_cast<uintptr_t>(sr) / 4) & 3u) : 0;
+        const int rid = (a0 - m) & 3;
+        IdsRaw<EPV> raw[RAG ? VPT : 1];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int32_t t = t0 + (j * 64 + lane) * EPV;
@@ -88,15 +91,13 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
 #pragma unroll
                     for (int r = 0; r < 4; ++r) id[j][4 * q + r] = (int32_t)s[r];
                 }
-            } else if (FULL || (t >= m && t + EPV <= Lv)) {  // every position inside the row
-                load_i32_shifted<EPV>(sr + (t - m), rid, id[j]);
-            } else {  // one id per position; -1 outside the row
-#pragma unroll
-                for (int e = 0; e < EPV; ++e) {
-                    const int32_t pos = t + e - m;
-                    id[j][e] = (pos >= 0 && pos < L) ? sr[pos] : -1;
-                }
+            } else {
+                ids_load<EPV, !FULL>(sr, L, t - m, rid, a0, raw[j]);
             }
+        }
+        if constexpr (RAG) {  // -1 outside the row
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) ids_shift<EPV, !FULL>(raw[j], L, t0 + (j * 64 + lane) * EPV - m, rid, id[j]);
         }
 #pragma unroll
         for (int i = 0; i < H; ++i) {
