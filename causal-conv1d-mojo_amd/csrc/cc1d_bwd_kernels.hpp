@@ -399,7 +399,12 @@ __device__ __forceinline__ void bwd_rows_compute_seq(const cc1d_bwd_params& p, i
     }
     if constexpr (RAG) {  // -1 outside the row
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) ids_shift<EPV, !FULL>(raw[j], Lr, t0 + (j * 64 + lane) * EPV - m, rid, id[j]);
+        for (int j = 0; j < VPT; ++j) {
+            const int32_t pos = t0 + (j * 64 + lane) * EPV - m;
+            const int32_t vs = t0 + j * 64 * EPV;  // vector j of lane 0: inside the row in every lane?
+            if (FULL || (vs >= m && vs + 64 * EPV <= L)) ids_shift<EPV, false>(raw[j], Lr, pos, rid, id[j]);
+            else ids_shift<EPV, true>(raw[j], Lr, pos, rid, id[j]);
+        }
     }
     int32_t hid[H], nid[H];
 #pragma unroll

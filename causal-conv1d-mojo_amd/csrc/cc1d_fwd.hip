@@ -97,7 +97,12 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
         }
         if constexpr (RAG) {  // -1 outside the row
 #pragma unroll
-            for (int j = 0; j < VPT; ++j) ids_shift<EPV, !FULL>(raw[j], L, t0 + (j * 64 + lane) * EPV - m, rid, id[j]);
+            for (int j = 0; j < VPT; ++j) {
+                const int32_t pos = t0 + (j * 64 + lane) * EPV - m;
+                const int32_t vs = t0 + j * 64 * EPV;  // vector j of lane 0: inside the row in every lane?
+                if (FULL || (vs >= m && vs + 64 * EPV <= Lv)) ids_shift<EPV, false>(raw[j], L, pos, rid, id[j]);
+                else ids_shift<EPV, true>(raw[j], L, pos, rid, id[j]);
+            }
         }
 #pragma unroll
         for (int i = 0; i < H; ++i) {
