@@ -197,11 +197,14 @@ def test_varlen_validation_codes(lib):
     assert call(batch=0) == OK
 
 
-def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4, offsets=(0, 0, 0)):
+def _workspace_floats(lib, B, D, L, dtype, channel_last=False, W=4, offsets=(0, 0, 0), seq_stride=None):
     p = _lib.BwdParams()
     fake = 1 << 20  # never dereferenced: the size is computed on the host
     p.x, p.dout, p.dx = (ctypes.c_void_p(fake + o) for o in offsets)  # byte offsets
     p.weight = ctypes.c_void_p(fake)
+    if seq_stride is not None:  # seq_idx (B, L) int32 with this time stride
+        p.seq_idx = ctypes.c_void_p(fake)
+        p.seq_idx_stride[:] = (L * seq_stride, seq_stride)
     p.batch, p.dim, p.seqlen, p.width = B, D, L, W
     strides = (D * L, 1, D) if channel_last else (D * L, L, 1)
     p.x_stride[:] = p.dout_stride[:] = p.dx_stride[:] = strides
@@ -251,3 +254,6 @@ def test_ragged_rows_keep_the_row_kernel(lib):
     # dout at another offset inside its vector than x: the generic kernel
     assert _workspace_floats(lib, B, D, 2047, bf16, offsets=(0, 2, 0)) == generic(2047) == 10240
     assert _workspace_floats(lib, B, D, 2048, bf16, offsets=(2, 2, 4)) == generic(2048) == 10240
+    # seq_idx: unit time stride keeps the row kernel; the ragged id loads need it, others go generic
+    assert _workspace_floats(lib, B, D, 2047, bf16, seq_stride=1) == rows(2047, 8) == 640
+    assert _workspace_floats(lib, B, D, 2047, bf16, seq_stride=2) == generic(2047) == 10240
