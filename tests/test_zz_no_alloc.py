@@ -64,6 +64,7 @@ CASES = [
     ("channel_last", (1, 4096, 8192), (3, 130, 515), torch.bfloat16),
     ("seq_idx", (2, 256, 4096), (2, 64, 333), torch.float16),
     ("states", (3, 192, 1000), (1, 40, 2), torch.float32),
+    ("ragged", (4, 512, 2041), (2, 96, 701), torch.bfloat16),  # odd lengths: ragged row kernels
 ]
 
 
