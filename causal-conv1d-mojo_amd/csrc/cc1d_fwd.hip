@@ -532,7 +532,15 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         // elements past a vector boundary
                         const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
                         const int64_t per = ceil_div(nvec, 64);
-                        const int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+                        int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+                        // a ragged row a little longer than a multiple of the
+                        // 4-vector segment would leave its last segment mostly
+                        // empty: 2 vectors per lane when that takes at most 85 %
+                        // of the lane slots (L = 2047: 34.2 instead of 37.6 us at
+                        // C2's batch and dim; aligned rows measured faster with 4)
+                        if (!aligned && vpt == 4 &&
+                            ceil_div(nvec, (int64_t)128) * 128 * 100 <= ceil_div(nvec, (int64_t)256) * 256 * 85)
+                            vpt = 2;
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
                         a.nseg_div = FastDiv((uint32_t)a.nseg);
