@@ -204,8 +204,8 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
                     c * p.final_states_stride[1];
 #pragma unroll
             for (int i = 0; i < H; ++i) {  // position L - H + i is window slot Lv + i - t
-                const float v = RAG ? pick<H + EPV>(win, Lv + i - t) : win[EPV + i];  // aligned: t + EPV == L
-                st(fs, i * p.final_states_stride[2], (L - H + i >= 0) ? v : 0.0f);
+                const float fv = RAG ? pick<H + EPV>(win, Lv + i - t) : win[EPV + i];  // aligned: t + EPV == L
+                st(fs, i * p.final_states_stride[2], (L - H + i >= 0) ? fv : 0.0f);
             }
         }
     }
