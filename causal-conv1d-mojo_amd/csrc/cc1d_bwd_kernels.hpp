@@ -1349,14 +1349,14 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
         const int64_t per = ceil_div(nvec, 64);
         pl.kind = kBwdRows;
-        pl.vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
-        // a row a little longer than a multiple of the segment would leave its
-        // last segment mostly empty: half the vectors per lane when that takes
-        // at most 85 % of the lane slots (at C2's batch and dim, L = 2056: 58.8
-        // instead of 65.7 us; 4104: 99.8 instead of 105.2; a ragged 1031, 1 vector
-        // per lane instead of 2: 47.5 instead of 51.2)
+        // vectors per lane (measured at C2's batch and dim): 4 from 129 vectors
+        // a row on -- one segment of 4 beats two of 2, the same lane slots
+        // (L = 1536: 38.8 instead of 45.2 us) -- except when a row a little longer
+        // than a multiple of the 4-vector segment would leave its last one
+        // mostly empty: 2 when that takes at most 85 % of the lane slots
+        // (L = 2056: 58.8 instead of 65.7 us; 4104: 99.8 instead of 105.2)
+        pl.vpt = per >= 3 ? 4 : (per == 2 ? 2 : 1);
         if (pl.vpt == 4 && ceil_div(nvec, 128) * 128 * 100 <= ceil_div(nvec, 256) * 256 * 85) pl.vpt = 2;
-        else if (pl.vpt == 2 && ceil_div(nvec, 64) * 64 * 100 <= ceil_div(nvec, 128) * 128 * 85) pl.vpt = 1;
         pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
         pl.a.n_items = p.batch * p.dim * pl.a.nseg;
         pl.a.nseg_div = FastDiv((uint32_t)pl.a.nseg);

@@ -533,13 +533,16 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         const int64_t nvec = aligned ? p.seqlen / EPV : ceil_div(p.seqlen + EPV - 1, EPV);
                         const int64_t per = ceil_div(nvec, 64);
                         int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
-                        // a ragged row a little longer than a multiple of the
-                        // 4-vector segment would leave its last segment mostly
-                        // empty: 2 vectors per lane when that takes at most 85 %
-                        // of the lane slots (L = 2047: 34.2 instead of 37.6 us at
-                        // C2's batch and dim; aligned rows measured faster with 4)
-                        if (!aligned && vpt == 4 &&
-                            ceil_div(nvec, (int64_t)128) * 128 * 100 <= ceil_div(nvec, (int64_t)256) * 256 * 85)
+                        // ragged rows (measured at C2's batch and dim; aligned ones
+                        // were faster without either): one segment of 4 vectors per
+                        // lane instead of two of 2 with the same lane slots (L = 1031:
+                        // 22.3 instead of 25.1 us), and 2 instead of 4 when a row a
+                        // little longer than a multiple of the 4-vector segment would
+                        // leave its last one mostly empty and 2 take at most 85 % of
+                        // the lane slots (L = 2047: 34.2 instead of 37.6 us)
+                        if (!aligned && per == 3) vpt = 4;
+                        else if (!aligned && vpt == 4 &&
+                                 ceil_div(nvec, (int64_t)128) * 128 * 100 <= ceil_div(nvec, (int64_t)256) * 256 * 85)
                             vpt = 2;
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
