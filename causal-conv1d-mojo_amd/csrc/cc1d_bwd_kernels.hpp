@@ -1351,11 +1351,14 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         pl.kind = kBwdRows;
         // vectors per lane (measured at C2's batch and dim): 4 from 129 vectors
         // a row on -- one segment of 4 beats two of 2, the same lane slots
-        // (L = 1536: 38.8 instead of 45.2 us) -- except when a row a little longer
+        // (L = 1536: 38.8 instead of 45.2 us), when the grid keeps 2048
+        // wavefronts (on smaller grids the more wavefronts of 2 measured faster)
+        // -- except when a row a little longer
         // than a multiple of the 4-vector segment would leave its last one
         // mostly empty: 2 when that takes at most 85 % of the lane slots
         // (L = 2056: 58.8 instead of 65.7 us; 4104: 99.8 instead of 105.2)
-        pl.vpt = per >= 3 ? 4 : (per == 2 ? 2 : 1);
+        const int64_t rows = p.batch * p.dim;
+        pl.vpt = per >= 4 || (per == 3 && rows >= 2048) ? 4 : (per >= 2 ? 2 : 1);
         if (pl.vpt == 4 && ceil_div(nvec, 128) * 128 * 100 <= ceil_div(nvec, 256) * 256 * 85) pl.vpt = 2;
         pl.a.nseg = ceil_div(nvec, 64 * (int64_t)pl.vpt);
         pl.a.n_items = p.batch * p.dim * pl.a.nseg;

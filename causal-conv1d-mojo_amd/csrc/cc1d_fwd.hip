@@ -535,12 +535,13 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         int vpt = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
                         // ragged rows (measured at C2's batch and dim; aligned ones
                         // were faster without either): one segment of 4 vectors per
-                        // lane instead of two of 2 with the same lane slots (L = 1031:
-                        // 22.3 instead of 25.1 us), and 2 instead of 4 when a row a
+                        // lane instead of two of 2 with the same lane slots when the
+                        // grid keeps 2048 wavefronts (L = 1031: 22.3 instead of
+                        // 25.1 us), and 2 instead of 4 when a row a
                         // little longer than a multiple of the 4-vector segment would
                         // leave its last one mostly empty and 2 take at most 85 % of
                         // the lane slots (L = 2047: 34.2 instead of 37.6 us)
-                        if (!aligned && per == 3) vpt = 4;
+                        if (!aligned && per == 3 && rows >= 2048) vpt = 4;
                         else if (!aligned && vpt == 4 &&
                                  ceil_div(nvec, (int64_t)128) * 128 * 100 <= ceil_div(nvec, (int64_t)256) * 256 * 85)
                             vpt = 2;

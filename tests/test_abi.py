@@ -233,10 +233,11 @@ def test_ragged_rows_keep_the_row_kernel(lib):
     64-step chunks. dout or dx at another offset modulo 16 bytes falls back to it."""
     B, D, W = 1, 64, 4
 
-    def rows(L, epv, aligned=False):
+    def rows(L, epv, aligned=False, B=B, D=D):
         nvec = L // epv if aligned else -(-(L + epv - 1) // epv)
         per = -(-nvec // 64)
-        vpt = 4 if per >= 3 else (2 if per == 2 else 1)  # one segment of 4 rather than two of 2
+        # one segment of 4 rather than two of 2 when the grid keeps 2048 wavefronts
+        vpt = 4 if per >= 4 or (per == 3 and B * D >= 2048) else (2 if per >= 2 else 1)
         if vpt == 4 and -(-nvec // 128) * 128 * 100 <= -(-nvec // 256) * 256 * 85:
             vpt = 2  # the last 4-vector segment would be mostly empty
         return B * D * -(-nvec // (64 * vpt)) * (W + 1)
@@ -248,8 +249,8 @@ def test_ragged_rows_keep_the_row_kernel(lib):
     assert _workspace_floats(lib, B, D, 2048, bf16) == rows(2048, 8, aligned=True) == 320
     assert _workspace_floats(lib, B, D, 2047, bf16) == rows(2047, 8) == 960  # 257 vectors: 3 of 128
     assert _workspace_floats(lib, B, D, 1001, bf16) == rows(1001, 8) == 320
-    assert _workspace_floats(lib, B, D, 1031, bf16) == rows(1031, 8) == 320  # 130 vectors: 1 segment of 256
-    assert _workspace_floats(lib, B, D, 1536, bf16) == rows(1536, 8, aligned=True) == 320
+    assert _workspace_floats(lib, B, D, 1031, bf16) == rows(1031, 8) == 640  # 130 vectors, 64 rows: 2 of 128
+    assert _workspace_floats(lib, 4, 5120, 1536, bf16) == rows(1536, 8, True, 4, 5120) == 102_400  # 1 of 256
     assert _workspace_floats(lib, B, D, 7, bf16) == rows(7, 8) == 320
     assert _workspace_floats(lib, B, D, 2047, fp32) == rows(2047, 4) == 1600
     # a base one element past a 16-byte boundary, x / dout / dx alike
