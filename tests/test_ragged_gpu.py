@@ -239,3 +239,21 @@ def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode, layout):
     _same_nonfinite_then_close(dx, rdx, dtype, "dx")
     _same_nonfinite_then_close(dw, rdw, dtype, "dweight", scale=sw)
     _same_nonfinite_then_close(db, rdb, dtype, "dbias", scale=sb)
+
+
+# the row planners' segment choices (4 vectors per lane from 129 vectors a row
+# when the grid keeps 2048 rows; 2 when a row just past a multiple of 256
+# vectors would leave its last 4-vector segment mostly empty), aligned and ragged
+SEGMENT_SHAPES = [(2, 1024, 1031), (2, 1024, 1032), (2, 1024, 1536), (1, 2048, 2047), (1, 2048, 2056),
+                  (1, 2048, 2100)]
+
+
+@pytest.mark.parametrize("shape", SEGMENT_SHAPES, ids=[f"B{b}D{d}L{l}" for b, d, l in SEGMENT_SHAPES])
+@pytest.mark.parametrize("mode", ["plain", "seq_idx"])
+def test_segment_choices(shape, mode):
+    B, D, L = shape
+    dtype = torch.bfloat16
+    x, w, b, _ = make_inputs(B, D, L, 4, dtype=dtype)
+    dout = make_inputs(B, D, L, 4, dtype=dtype, seed=1)[0]
+    seq = seq_pattern("random_runs", B, L) if mode == "seq_idx" else None
+    _check_all(_autograd(x, w, b, dout, seq_idx=seq), x, w, b, dout, dtype, seq_idx=seq)
