@@ -545,10 +545,12 @@ int launch_fwd(const cc1d_fwd_params& p, hipStream_t stream) {
                         else if (!aligned && vpt == 4 &&
                                  ceil_div(nvec, (int64_t)128) * 128 * 100 <= ceil_div(nvec, (int64_t)256) * 256 * 85)
                             vpt = 2;
-                        // a grid of fewer than 2048 wavefronts (2 per SIMD) with 4
-                        // vectors per lane: 2 give twice the wavefronts (B = 1,
-                        // D = 768, L = 2048: 3.16 instead of 3.41 us)
+                        // a grid of fewer than 2048 wavefronts (2 per SIMD): half the
+                        // vectors per lane, twice the wavefronts (B = 1, D = 768,
+                        // L = 2048: 3.03 instead of 3.41 us; D = 512, L = 1024:
+                        // 2.40 instead of 2.53)
                         if (vpt == 4 && rows * ceil_div(nvec, (int64_t)256) < 2048) vpt = 2;
+                        if (vpt == 2 && rows * ceil_div(nvec, (int64_t)128) < 2048) vpt = 1;
                         a.nseg = ceil_div(nvec, 64 * (int64_t)vpt);
                         a.n_items = rows * a.nseg;
                         a.nseg_div = FastDiv((uint32_t)a.nseg);
