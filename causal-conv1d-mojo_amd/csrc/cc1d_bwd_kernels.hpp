@@ -51,7 +51,9 @@ struct BwdArgs {
 constexpr int kRowsWPB = 4;
 // channel-last walk: time steps per chunk, per wavefront run, runs per block
 constexpr int kClG = 4;
-constexpr int kClR = 128;
+constexpr int kClR = 128;      // run length, and the shorter ones for small grids
+constexpr int kClRMid = 32;
+constexpr int kClRShort = 16;
 constexpr int kClWPB = 8;
 
 // Registers of one wavefront-segment of a row: VPT 16-byte vectors of x and
@@ -1373,8 +1375,20 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         pl.kind = kBwdCl;
         pl.cpl = CPL;
         pl.a.groups = ceil_div(p.dim / CPL, 64);
-        pl.a.chunk = kClR;
-        pl.a.nseg = ceil_div(p.seqlen, kClR * kClWPB);  // run groups per row
+        // run length: a wavefront walks its run chunk by chunk, each chunk's
+        // loads in flight behind the previous one's arithmetic, so a run takes
+        // about the same time at any problem size (memory latency per chunk);
+        // the longest run that still gives 2048 wavefronts (2 per SIMD), else
+        // the shortest (measured, bf16, B = 1: D = 4096, L = 8192 keeps 128;
+        // D = 1536, L = 2048: 9.1 us with 16 against 34.9 with 128)
+        pl.a.chunk = kClRShort;
+        for (const int r : {kClR, kClRMid}) {
+            if (p.batch * pl.a.groups * ceil_div(p.seqlen, (int64_t)r) >= 2048) {
+                pl.a.chunk = r;
+                break;
+            }
+        }
+        pl.a.nseg = ceil_div(p.seqlen, pl.a.chunk * kClWPB);  // run groups per row
         pl.a.n_items = 0;
         pl.blocks = p.batch * pl.a.groups * pl.a.nseg;
         pl.records = pl.blocks;
@@ -1413,7 +1427,10 @@ int launch_plan(const BwdPlan& pl, const cc1d_bwd_params& p, hipStream_t stream)
         return with_flag(p.seq_idx != nullptr, [&](auto qc) {
             constexpr bool SEQ = decltype(qc)::value;
             constexpr int G = W - 1 <= kClG ? kClG : 2 * kClG;  // at least H steps per chunk
-            return launch(bwd_clw<T, W, G, kClR, kClWPB, SILU, SEQ>, grid, dim3(64 * kClWPB), stream, a);
+            const dim3 block(64 * kClWPB);
+            if (a.chunk == kClRShort) return launch(bwd_clw<T, W, G, kClRShort, kClWPB, SILU, SEQ>, grid, block, stream, a);
+            if (a.chunk == kClRMid) return launch(bwd_clw<T, W, G, kClRMid, kClWPB, SILU, SEQ>, grid, block, stream, a);
+            return launch(bwd_clw<T, W, G, kClR, kClWPB, SILU, SEQ>, grid, block, stream, a);
         });
     }
     return launch(bwd_generic<T, W, SILU>, grid, dim3(256), stream, a);

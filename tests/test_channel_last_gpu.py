@@ -168,6 +168,30 @@ def test_cl_backward_many_tile_groups():
            scales(x, w, b, dout, activation="silu"))
 
 
+# the channel-last backward walks runs of the longest of 128, 32 and 16 steps
+# that gives 2048 wavefronts (a wavefront per 64 lanes' channels and run):
+# one shape per run length, the sequence ending inside a run
+_RUN_SHAPES = {"run128": (2, 1024, 16392), "run32": (2, 1024, 4136), "run16": (1, 768, 2050)}
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("run", list(_RUN_SHAPES))
+@pytest.mark.parametrize("mode", ["plain", "seq_idx", "states"])
+def test_cl_backward_run_lengths(dtype, run, mode):
+    B, D, L = _RUN_SHAPES[run]
+    if dtype == torch.float32:
+        D //= 2  # one channel per lane instead of two: the same wavefronts
+    x, w, b, init = make_inputs(B, D, L, 4, dtype=dtype, has_init=True)
+    dout = make_inputs(B, D, L, 4, dtype=dtype, seed=1)[0]
+    if mode != "states":
+        init = None
+    dfs = make_inputs(B, D, 3, 4, dtype=dtype, seed=2)[0] if mode == "states" else None
+    s = seq_pattern("random_runs", B, L) if mode == "seq_idx" else None
+    got = _grads(x, w, b, dout, init=init, seq_idx=s, dfs=dfs)
+    ref = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=s, initial_states=init, dfinal_states=dfs, activation="silu")
+    _check(got, ref, dtype, scales(x, w, b, dout, init=init, seq_idx=s, activation="silu"), has_init=init is not None)
+
+
 # sequence starts on and next to the edges of 4- and 8-step chunks, 128-step runs and
 # 1024-step blocks, a padding stretch (-1) across a run edge, and an id that comes back
 _EDGE_CUTS = [1, 3, 4, 127, 128, 131, 700, 1021, 1024, 1025, 1600, 2047, 2048, 2300]
