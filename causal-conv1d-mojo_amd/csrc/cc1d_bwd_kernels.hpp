@@ -52,7 +52,7 @@ constexpr int kRowsWPB = 4;
 // channel-last walk: time steps per chunk, per wavefront run, runs per block
 constexpr int kClG = 4;
 constexpr int kClR = 128;      // run length, and the shorter ones for small grids
-constexpr int kClRMid = 32;
+constexpr int kClRMid = 64;
 constexpr int kClRShort = 16;
 constexpr int kClWPB = 8;
 
@@ -1380,7 +1380,8 @@ BwdPlan plan_bwd(const cc1d_bwd_params& p) {
         // about the same time at any problem size (memory latency per chunk);
         // the longest run that still gives 2048 wavefronts (2 per SIMD), else
         // the shortest (measured, bf16, B = 1: D = 4096, L = 8192 keeps 128;
-        // D = 1536, L = 2048: 9.1 us with 16 against 34.9 with 128)
+        // D = 4096, L = 4096: 24.9 us with 64 against 35.2 with 128; D = 1536,
+        // L = 2048: 9.1 us with 16 against 34.9 with 128)
         pl.a.chunk = kClRShort;
         for (const int r : {kClR, kClRMid}) {
             if (p.batch * pl.a.groups * ceil_div(p.seqlen, (int64_t)r) >= 2048) {

@@ -168,10 +168,10 @@ def test_cl_backward_many_tile_groups():
            scales(x, w, b, dout, activation="silu"))
 
 
-# the channel-last backward walks runs of the longest of 128, 32 and 16 steps
+# the channel-last backward walks runs of the longest of 128, 64 and 16 steps
 # that gives 2048 wavefronts (a wavefront per 64 lanes' channels and run):
 # one shape per run length, the sequence ending inside a run
-_RUN_SHAPES = {"run128": (2, 1024, 16392), "run32": (2, 1024, 4136), "run16": (1, 768, 2050)}
+_RUN_SHAPES = {"run128": (2, 1024, 16392), "run64": (2, 1024, 8200), "run16": (1, 768, 2050)}
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
