@@ -133,16 +133,19 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
         }
         // a ragged row's first vector holds m elements of the previous row:
         // they are positions -m .. -1 of this one (x: initial_states or zero;
-        // dout: zero)
+        // dout: zero), merged in as raw bits
         if (RAG && !FULL && t0 == 0 && m > 0 && lane == 0) {
-            float fx[EPV], fg[EPV];
+            constexpr int EPD = EPV / 4;  // elements per dword
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                fx[e] = e >= m ? vget<T>(r.v[0], e) : pick<H>(hinit, e - m + H);
-                fg[e] = e >= m ? vget<T>(r.gv[0], e) : 0.0f;
+            for (int d = 0; d < 4; ++d) {
+                uint32_t ib = 0;
+#pragma unroll
+                for (int k = 0; k < EPD; ++k)
+                    ib |= tbits<T>(pick<H>(hinit, d * EPD + k - m + H)) << (32 / EPD * k);
+                const uint32_t keep = ~lead_mask<T>(d, m);
+                r.v[0][d] = (r.v[0][d] & keep) | (ib & ~keep);
+                r.gv[0][d] &= keep;
             }
-            r.v[0] = vpack<T>(fx);
-            r.gv[0] = vpack<T>(fg);
         }
         const auto& v = r.v;
         const auto& gv = r.gv;
@@ -254,19 +257,40 @@ __device__ __forceinline__ void bwd_rows_compute(const cc1d_bwd_params& p, int l
             }
             if constexpr (!RAG) {
                 if (FULL || t < L) vstore_nt(dxr + t, vpack<T>(o));
-            } else if (FULL || (t >= m && t + EPV <= L)) {
-                vstore_nt(dxr + t, vpack<T>(o));
-            } else if (t < L) {  // a vector shared with a neighbouring row
+            } else {
+                const u32x4 ov = vpack<T>(o);
+                if (FULL || (t >= m && t + EPV <= L)) {
+                    vstore_nt(dxr + t, ov);
+                } else if (t < L) {  // a vector shared with a neighbouring row
 #pragma unroll
-                for (int e = 0; e < EPV; ++e)
-                    if (t + e >= m && t + e < L) st(dxr, t + e, o[e]);
+                    for (int e = 0; e < EPV; ++e)
+                        if ((uint32_t)(t + e - m) < (uint32_t)p.seqlen) st_elem<T>(dxr + t + e, ov, e);
+                }
             }
         };
 
         float dp[2][EPV];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            if constexpr (RAG && !FULL) {
+            if constexpr (RAG && !FULL && SILU) {
+                // With SiLU, x and dout zeroed past the row's end (and before its
+                // start, above) make every outside position's dpre an exact zero
+                // whenever the row's own values are finite; where they are not,
+                // the reference's weight and bias gradients are NaN as well (the
+                // SiLU derivative at a non-finite pre is NaN). So no position
+                // needs a mask of its own. Wave-uniform test: vector j may hold
+                // positions past the end.
+                if (t0 + (j + 1) * 64 * EPV > L) {
+                    const int32_t t = t0 + (j * 64 + lane) * EPV;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t keep = lead_mask<T>(d, L - t);
+                        r.v[j][d] &= keep;
+                        r.gv[j][d] &= keep;
+                    }
+                }
+                dpre_vec(j, dp[j & 1], std::false_type{});
+            } else if constexpr (RAG && !FULL) {
                 // a ragged row's segments are not full, but only their first and
                 // last vectors hold positions outside the row (wave-uniform test)
                 const int32_t vs = t0 + j * 64 * EPV;  // vector j of lane 0

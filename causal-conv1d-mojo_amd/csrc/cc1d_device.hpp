@@ -200,6 +200,23 @@ template <typename T> __device__ __forceinline__ u32x4 vload_uniform(const T* p)
 }
 template <typename T> __device__ __forceinline__ void st(T* p, int64_t i, float v) { p[i] = from_f32<T>(v); }
 
+// Dword d of a 16-byte vector of T: the bits of its elements e < n (all of
+// them for n >= EPV, none for n <= 0).
+template <typename T> __device__ __forceinline__ uint32_t lead_mask(int d, int32_t n) {
+    if constexpr (sizeof(T) == 4) return d < n ? ~0u : 0u;
+    else return 2 * d + 1 < n ? ~0u : (2 * d < n ? 0xffffu : 0u);
+}
+// Storage bits of an fp32 value that T represents exactly.
+template <typename T> __device__ __forceinline__ uint32_t tbits(float v) {
+    if constexpr (sizeof(T) == 4) return __float_as_uint(v);
+    else return from_f32<T>(v).bits;
+}
+// Store element e of the packed vector v at p (its raw bits: no rounding).
+template <typename T> __device__ __forceinline__ void st_elem(T* p, const u32x4& v, int e) {
+    if constexpr (sizeof(T) == 4) *reinterpret_cast<uint32_t*>(p) = v[e];
+    else *reinterpret_cast<uint16_t*>(p) = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+}
+
 // a[k] for a runtime k (0 outside [0, N)), as a chain of selects: a register
 // array indexed at run time would be placed in scratch memory
 template <int N> __device__ __forceinline__ float pick(const float* a, int k) {
