@@ -188,12 +188,15 @@ __device__ __forceinline__ void fwd_rows_segment(const cc1d_fwd_params& p, int l
         }
         if constexpr (!RAG) {
             if (FULL || t < L) vstore_nt(orow + t, vpack<T>(o));
-        } else if (FULL || (t >= m && t + EPV <= Lv)) {
-            vstore_nt(orow + t, vpack<T>(o));
-        } else if (t < Lv) {  // a vector shared with a neighbouring row
+        } else {
+            const u32x4 ov = vpack<T>(o);
+            if (FULL || (t >= m && t + EPV <= Lv)) {
+                vstore_nt(orow + t, ov);
+            } else if (t < Lv) {  // a vector shared with a neighbouring row
 #pragma unroll
-            for (int e = 0; e < EPV; ++e)
-                if (t + e >= m && t + e < Lv) st(orow, t + e, o[e]);
+                for (int e = 0; e < EPV; ++e)
+                    if ((uint32_t)(t + e - m) < (uint32_t)(Lv - m)) st_elem<T>(orow + t + e, ov, e);
+            }
         }
 
         // final_states (_fn.py:31-50): the lane holding the row's last
