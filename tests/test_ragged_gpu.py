@@ -241,6 +241,38 @@ def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode, layout):
     _same_nonfinite_then_close(db, rdb, dtype, "dbias", scale=sb)
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("seqlen", [5, 1021, 1032])
+@pytest.mark.parametrize("activation", [None, "silu"])
+def test_nonfinite_initial_states(dtype, seqlen, activation):
+    """Channel 1's initial_states hold inf in the slot next to the row, channel 4's a NaN in the
+    farthest slot. A ragged row's first vector holds the previous row's elements, which read as
+    these states; with SiLU the positions before the row then have an exact zero dpre only
+    for finite states, and the reference's weight and bias gradients are NaN for the others.
+    Every entry the reference makes non-finite is non-finite here, the rest match it (5, 1021:
+    ragged rows; 1032: aligned)."""
+    B, D, W = 2, 6, 4
+    x, w, b, init = make_inputs(B, D, seqlen, W, dtype=dtype, has_init=True)
+    dout = make_inputs(B, D, seqlen, W, dtype=dtype, seed=1)[0]
+    clean = init.clone()
+    init[:, 1, -1] = float("inf")
+    init[:, 4, 0] = float("nan")
+    clean[:, 1, -1] = 0
+    clean[:, 4, 0] = 0
+    out, _, dx, dw, db, di = _autograd(x, w, b, dout, init=init, activation=activation)
+    rout = O.causal_conv1d_fn(x, w, b, initial_states=init, activation=activation)
+    rdx, rdw, rdb, rdi = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init, activation=activation)
+    sw, sb = scales(x, w, b, dout, init=clean, activation=activation)
+    ok = [c for c in range(D) if c not in (1, 4)]
+    assert torch.isfinite(rdw[ok].double()).all() and not torch.isfinite(rout[:, 1].double()).all(), \
+        "the case is what it says"
+    _same_nonfinite_then_close(out, rout, dtype, "out")
+    _same_nonfinite_then_close(dx, rdx, dtype, "dx")
+    _same_nonfinite_then_close(dw, rdw, dtype, "dweight", scale=sw)
+    _same_nonfinite_then_close(db, rdb, dtype, "dbias", scale=sb)
+    _same_nonfinite_then_close(di, rdi, dtype, "dinitial_states")
+
+
 # the row planners' segment choices (4 vectors per lane from 129 vectors a row
 # when the grid keeps 2048 rows; 2 when a row just past a multiple of 256
 # vectors would leave its last 4-vector segment mostly empty), aligned and ragged
