@@ -739,8 +739,9 @@ __device__ __forceinline__ void bwd_chunk(const cc1d_bwd_params& p, int64_t b, i
         if (s < t1) {
             pb += d;
 #pragma unroll
-            for (int k = 0; k < W; ++k)
-                if (sr == nullptr || iw[k] == iw[H]) pw[k] = __builtin_fmaf(d, xw[k], pw[k]);
+            for (int k = 0; k < W; ++k)  // a tap before the row adds a term only with initial_states
+                if ((sr == nullptr || iw[k] == iw[H]) && (ir != nullptr || s + k >= H))
+                    pw[k] = __builtin_fmaf(d, xw[k], pw[k]);
 #pragma unroll
             for (int i = 0; i < H; ++i)
                 if (s == i) dfirst[i] = d;
@@ -1096,14 +1097,16 @@ __global__ void __launch_bounds__(64 * WPB) bwd_clw(const BwdArgs a) {
                     if (dead) d = 0.0f;
                     dn[e] = d;
                     // a step past the end adds no term (zero dpre times a
-                    // non-finite x of the window would be NaN); padding
-                    // inside the sequence adds its zero terms, as the
-                    // reference does (wave-uniform test)
+                    // non-finite x of the window would be NaN), nor does a tap
+                    // before the row without initial_states; padding inside
+                    // the sequence adds its zero terms, as the reference does
+                    // (wave-uniform tests)
                     if (ACC && in) {
                         s.pb[e] += d;
 #pragma unroll
                         for (int k = 0; k < H; ++k)
-                            if (idk[k] == idp) s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
+                            if (idk[k] == idp && (pos + k >= H || p.initial_states != nullptr))
+                                s.pw[k][e] = __builtin_fmaf(d, s.xw[k][e], s.pw[k][e]);
                         s.pw[H][e] = __builtin_fmaf(d, xc[e], s.pw[H][e]);
                     }
                 }

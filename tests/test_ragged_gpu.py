@@ -213,29 +213,60 @@ _LAYOUTS = {
 @pytest.mark.parametrize("mode", ["linear", "silu", "seq_idx"])
 @pytest.mark.parametrize("layout", list(_LAYOUTS))
 def test_nonfinite_neighbours_do_not_leak(dtype, seqlen, mode, layout):
-    """Channel 2 ends in inf, channel 5 starts with NaN, channel 8 is NaN throughout. Rows: each
-    shares vectors with its neighbours (1021: ragged rows), or is the last row of a segment
-    that lies past the row's end (1032: aligned rows). Channel-last: the last run of 128 steps
-    reaches past the end. Only the entries that the reference makes non-finite may be
-    non-finite; everything else matches it."""
+    """x: channel 2 ends in inf, channel 5 starts with NaN, channel 8 is NaN throughout; dout
+    ends in inf in channel 3 and is NaN throughout channel 10. Rows: each shares vectors with
+    its neighbours (1021: ragged rows), or is the last row of a segment that lies past the
+    row's end (1032: aligned rows). Channel-last: the last run of 128 steps reaches past the
+    end. Only the entries that the reference makes non-finite may be non-finite; everything
+    else matches it."""
     B, D, W = 2, 12, 4
     x, w, b, _ = make_inputs(B, D, seqlen, W, dtype=dtype)
     dout = make_inputs(B, D, seqlen, W, dtype=dtype, seed=1)[0]
-    clean = x.clone()
     x[:, 2, -1] = float("inf")
     x[:, 5, 0] = float("nan")
     x[:, 8, :] = float("nan")
-    for c in (2, 5, 8):
-        clean[:, c] = 0
+    dout[:, 3, -1] = float("inf")
+    dout[:, 10, :] = float("nan")
+    clean, gclean = (torch.where(torch.isfinite(t), t, torch.zeros_like(t)) for t in (x, dout))
     act = "silu" if mode != "linear" else None
     seq = _leading_padding(B, seqlen) if mode == "seq_idx" else None
     out, _, dx, dw, db, _ = _autograd(x, w, b, dout, seq_idx=seq, activation=act, view=_LAYOUTS[layout])
     rout = O.causal_conv1d_fn(x, w, b, seq_idx=seq, activation=act)
     rdx, rdw, rdb, _ = O.causal_conv1d_bwd(x, w, b, dout, seq_idx=seq, activation=act)
-    sw, sb = scales(clean, w, b, dout, seq_idx=seq, activation=act)
-    ok = [c for c in range(D) if c not in (2, 5, 8)]
+    sw, sb = scales(clean, w, b, gclean, seq_idx=seq, activation=act)
+    ok = [c for c in range(D) if c not in (2, 3, 5, 8, 10)]
     assert torch.isfinite(rdw[ok].double()).all(), "the case is what it says"
     _same_nonfinite_then_close(out, rout, dtype, "out")
+    _same_nonfinite_then_close(dx, rdx, dtype, "dx")
+    _same_nonfinite_then_close(dw, rdw, dtype, "dweight", scale=sw)
+    _same_nonfinite_then_close(db, rdb, dtype, "dbias", scale=sb)
+
+
+_ROW_HEAD_REASON = ("row kernels add a row's first W-1 dpre times the zeros before the row for "
+                    "taps the reference skips without initial_states; a non-finite dpre there "
+                    "makes all of that channel's weight gradient NaN instead of the taps "
+                    "reaching into the row (the exact forms measured cost the kernel a "
+                    "wavefront per SIMD)")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
+@pytest.mark.parametrize("seqlen", [1021, 1032])
+@pytest.mark.parametrize("activation", [None, "silu"])
+@pytest.mark.parametrize("layout", [pytest.param("rows", marks=pytest.mark.xfail(strict=True, reason=_ROW_HEAD_REASON)),
+                                    "channel_last", "strided"])
+def test_nonfinite_dout_at_a_rows_start(dtype, seqlen, activation, layout):
+    """dout of channel 6 starts with NaN, no initial_states: the reference's weight gradient is
+    NaN only in the tap that reaches the row's first x (bwd_full_cpu/kernel.mojo:264-274 skip
+    the taps before the row), the rest of that channel's and every other channel's match."""
+    B, D, W = 2, 12, 4
+    x, w, b, _ = make_inputs(B, D, seqlen, W, dtype=dtype)
+    dout = make_inputs(B, D, seqlen, W, dtype=dtype, seed=1)[0]
+    dout[:, 6, 0] = float("nan")
+    gclean = torch.where(torch.isfinite(dout), dout, torch.zeros_like(dout))
+    _, _, dx, dw, db, _ = _autograd(x, w, b, dout, activation=activation, view=_LAYOUTS[layout])
+    rdx, rdw, rdb, _ = O.causal_conv1d_bwd(x, w, b, dout, activation=activation)
+    sw, sb = scales(x, w, b, gclean, activation=activation)
+    assert int((~torch.isfinite(rdw[6].double())).sum()) == 1, "the case is what it says"
     _same_nonfinite_then_close(dx, rdx, dtype, "dx")
     _same_nonfinite_then_close(dw, rdw, dtype, "dweight", scale=sw)
     _same_nonfinite_then_close(db, rdb, dtype, "dbias", scale=sb)
