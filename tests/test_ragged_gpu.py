@@ -275,13 +275,15 @@ def test_nonfinite_dout_at_a_rows_start(dtype, seqlen, activation, layout):
 @pytest.mark.parametrize("dtype", DTYPES, ids=DTYPE_IDS)
 @pytest.mark.parametrize("seqlen", [5, 1021, 1032])
 @pytest.mark.parametrize("activation", [None, "silu"])
-def test_nonfinite_initial_states(dtype, seqlen, activation):
+@pytest.mark.parametrize("layout", ["rows", "channel_last", "strided"])
+def test_nonfinite_initial_states(dtype, seqlen, activation, layout):
     """Channel 1's initial_states hold inf in the slot next to the row, channel 4's a NaN in the
     farthest slot. A ragged row's first vector holds the previous row's elements, which read as
     these states; with SiLU the positions before the row then have an exact zero dpre only
     for finite states, and the reference's weight and bias gradients are NaN for the others.
     Every entry the reference makes non-finite is non-finite here, the rest match it (5, 1021:
-    ragged rows; 1032: aligned)."""
+    ragged rows; 1032: aligned; the channel-last and generic kernels take the states as their
+    first window)."""
     B, D, W = 2, 6, 4
     x, w, b, init = make_inputs(B, D, seqlen, W, dtype=dtype, has_init=True)
     dout = make_inputs(B, D, seqlen, W, dtype=dtype, seed=1)[0]
@@ -290,7 +292,8 @@ def test_nonfinite_initial_states(dtype, seqlen, activation):
     init[:, 4, 0] = float("nan")
     clean[:, 1, -1] = 0
     clean[:, 4, 0] = 0
-    out, _, dx, dw, db, di = _autograd(x, w, b, dout, init=init, activation=activation)
+    out, _, dx, dw, db, di = _autograd(x, w, b, dout, init=init, activation=activation,
+                                       view=_LAYOUTS[layout])
     rout = O.causal_conv1d_fn(x, w, b, initial_states=init, activation=activation)
     rdx, rdw, rdb, rdi = O.causal_conv1d_bwd(x, w, b, dout, initial_states=init, activation=activation)
     sw, sb = scales(x, w, b, dout, init=clean, activation=activation)
